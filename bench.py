@@ -1,0 +1,228 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention path on BASELINE.json's shapes.
+
+One "step" is one call of the hot path over one batch of synthetic input
+(seeded, generated on the GPU; see pelica_amd/workloads.py).  The headline
+workload is config 3: gpt-oss-20b decode attention at 32K context, full
+layer with sinks (value = KV GB/s).  Prefill (config 4, TFLOP/s) and the
+other configs are reported beside it in the same JSON line.
+
+Inputs are resident in HBM before the timed region; each step reads a
+different copy of the KV cache (copies totalling >= 1 GiB), so the 256 MB
+last-level cache cannot serve the bytes the HBM roofline counts.
+
+The CPU baseline is the C port of the reference's cpu_attn.rs (oracle/,
+kind "port") timed on this host's cores on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+F16_PEAK_TFLOPS = 2500.0    # MI355X dense f16 MFMA
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default="", help="comma list of config names to time (default: all)")
+    return ap.parse_args()
+
+
+def rotating_copies(t, min_total=1 << 30):
+    import torch
+
+    n = max(1, -(-min_total // (t.numel() * t.element_size())))
+    return [t] + [t.clone() for _ in range(n - 1)]
+
+
+def time_calls(fn, n_copies, steps, warmup):
+    """Events on the launch stream around `steps` calls; returns ms per call."""
+    import torch
+
+    for i in range(warmup):
+        fn(i % n_copies)
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for i in range(steps):
+        fn(i % n_copies)
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def bench_decode(cfg, steps, warmup):
+    import torch
+
+    from pelica_amd import attn
+    from pelica_amd import workloads as wl
+
+    inp = wl.make_inputs(cfg, "cuda")
+    ks = rotating_copies(inp.k)
+    vs = [inp.v] + [inp.v.clone() for _ in range(len(ks) - 1)]
+    out = torch.empty_like(inp.q)
+    kw = dict(n_kv=cfg.n_kv, kv_len=inp.kv_len, sinks=inp.sinks, window=cfg.window)
+    if inp.ragged:
+        kw.update(seq_kv_len=inp.seq_len, seq_kv_offset=inp.seq_off)
+    desc = attn.make_desc(cfg.n_head, cfg.n_kv, cfg.hd, n_seq=cfg.n_seq, q_tokens=cfg.q_tokens,
+                          kv_len=inp.kv_len, seq_kv_len=kw.get("seq_kv_len"), seq_kv_offset=kw.get("seq_kv_offset"),
+                          window=cfg.window)
+    ws_n = attn.workspace_bytes(desc)
+    ws = torch.empty(max(ws_n, 16), dtype=torch.uint8, device="cuda")
+
+    def call(i):
+        attn.decode(inp.q, ks[i], vs[i], out=out, workspace=ws, **kw)
+
+    ms = time_calls(call, len(ks), steps, warmup)
+    nbytes = wl.kv_bytes(cfg, inp.seq_len.tolist())
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return dict(config=cfg.name, ms=ms, bytes=nbytes, GBps=gbs, frac_hbm=gbs / HBM_PEAK_GBS,
+                workspace_bytes=ws_n, kv_copies=len(ks))
+
+
+def bench_prefill(cfg, steps, warmup):
+    import torch
+
+    from pelica_amd import attn
+    from pelica_amd import workloads as wl
+
+    inp = wl.make_inputs(cfg, "cuda")
+    out = torch.empty_like(inp.q)
+
+    def call(i):
+        attn.prefill(inp.q, inp.k, inp.v, n_kv=cfg.n_kv, kv_len=inp.kv_len, sinks=inp.sinks, window=cfg.window,
+                     out=out)
+
+    ms = time_calls(call, 1, steps, warmup)
+    flops = wl.attn_flops(cfg)
+    tf = flops / (ms * 1e-3) / 1e12
+    return dict(config=cfg.name, ms=ms, flops=flops, TFLOPs=tf, frac_mfma=tf / F16_PEAK_TFLOPS)
+
+
+def cpu_baseline_decode(cfg, reps=5):
+    """The C port of cpu_attn.rs on every host core, full C3 workload."""
+    import numpy as np
+
+    from oracle import oracle as orc
+    from pelica_amd import workloads as wl
+
+    inp = wl.make_inputs(cfg, "cpu")
+    q = inp.q.numpy()
+    k = inp.k.numpy().view(np.uint16)
+    v = inp.v.numpy().view(np.uint16)
+    sinks = inp.sinks.numpy() if inp.sinks is not None else None
+    threads = os.cpu_count() or 1
+    orc.attention(q, k, v, n_kv=cfg.n_kv, kv_len=cfg.kv_len, sinks=sinks, window=cfg.window, threads=threads)
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        orc.attention(q, k, v, n_kv=cfg.n_kv, kv_len=cfg.kv_len, sinks=sinks, window=cfg.window, threads=threads)
+        times.append(time.perf_counter() - t)
+    sec = float(np.median(times))
+    return dict(value=wl.kv_bytes(cfg) / sec / 1e9, unit="GB/s", cores=threads, kind="port",
+                sample=f"full {cfg.name} call (64 query heads x 32768 keys), median of {reps}",
+                ms=sec * 1e3)
+
+
+def cpu_baseline_prefill(cfg, rows=32):
+    """The same port on the last `rows` prompt tokens (the longest key ranges)."""
+    import numpy as np
+
+    from oracle import oracle as orc
+    from pelica_amd import workloads as wl
+
+    inp = wl.make_inputs(cfg, "cpu")
+    q = inp.q.numpy().view(np.uint16)
+    k = inp.k.numpy().view(np.uint16)
+    v = inp.v.numpy().view(np.uint16)
+    sinks = inp.sinks.numpy()
+    T = cfg.q_tokens
+    threads = os.cpu_count() or 1
+    t = time.perf_counter()
+    orc.attention(q, k, v, n_kv=cfg.n_kv, kv_len=cfg.kv_len, sinks=sinks, window=cfg.window, t_begin=T - rows,
+                  t_end=T, threads=threads)
+    sec = time.perf_counter() - t
+    pairs = sum(min(p + 1, cfg.window) if cfg.window else p + 1 for p in range(T - rows, T))
+    flops = 4 * cfg.hd * cfg.n_head * pairs
+    return dict(value=flops / sec / 1e12, unit="TFLOP/s", cores=threads, kind="port",
+                sample=f"last {rows} of {T} prompt tokens of {cfg.name}", ms=sec * 1e3)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); "
+              "the attention path is measured at its single-GPU shape", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from pelica_amd import workloads as wl
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    only = set(filter(None, args.only.split(",")))
+
+    def want(c):
+        return not only or c.name in only
+
+    results = {}
+    for cfg in (wl.C3_FULL, wl.C3_SWA, wl.C1, wl.C2, wl.C5):
+        if want(cfg):
+            results[cfg.name] = bench_decode(cfg, args.steps, args.warmup)
+    for cfg in (wl.C4_FULL, wl.C4_SWA):
+        if want(cfg):
+            results[cfg.name] = bench_prefill(cfg, args.steps, args.warmup)
+
+    head = results.get(wl.C3_FULL.name)
+    pre = results.get(wl.C4_FULL.name)
+    cpu = None if args.no_cpu else cpu_baseline_decode(wl.C3_FULL)
+    cpu_pre = None if args.no_cpu else cpu_baseline_prefill(wl.C4_FULL)
+    line = {
+        "metric": "decode-attn KV GB/s (% HBM peak); prefill-attn TFLOP/s (% MFMA peak)",
+        "value": round(head["GBps"], 1) if head else None,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms"], 5) if head else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 KV, f32 softmax/accumulate",
+        "data": "synthetic (seeded N(0,1) per BASELINE.json configs)",
+        "config": {"workload": wl.C3_FULL.name, "n_head": 64, "n_kv": 8, "hd": 64, "kv_len": 32768,
+                   "sinks": True, "window": 0, "batch": 1},
+        "roofline": None,
+        "cpu_baseline": cpu,
+        "prefill": None,
+        "configs": {k: {kk: (round(vv, 6) if isinstance(vv, float) else vv) for kk, vv in r.items()}
+                    for k, r in results.items()},
+    }
+    if head:
+        line["roofline"] = {"bound": "hbm", "achieved": round(head["GBps"], 1), "peak": HBM_PEAK_GBS,
+                            "unit": "GB/s", "frac": round(head["frac_hbm"], 4), "traffic": None,
+                            "kernel": "decode call (split + combine), HIP events per call"}
+    if pre:
+        line["prefill"] = {"workload": wl.C4_FULL.name, "value": round(pre["TFLOPs"], 1), "unit": "TFLOP/s",
+                           "ms_per_step": round(pre["ms"], 5),
+                           "roofline": {"bound": "mfma", "achieved": round(pre["TFLOPs"], 1),
+                                        "peak": F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                        "frac": round(pre["frac_mfma"], 4), "traffic": None},
+                           "cpu_baseline": cpu_pre}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

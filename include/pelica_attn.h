@@ -1,0 +1,110 @@
+/* pelica_attn — MI355X (gfx950) attention for Pelica's decode and prefill
+ * passes, behind a plain C ABI.
+ *
+ * All tensor pointers are DEVICE pointers owned by the caller; every call is
+ * asynchronous on `stream` (a hipStream_t passed as void*, NULL = the null
+ * stream).  No call allocates device memory except through the caller's
+ * workspace.  No C++ exception crosses this boundary: every entry point
+ * returns a status (0 ok, negative error) and the message of the calling
+ * thread's last error is available from pelica_attn_last_error().
+ *
+ * Layouts (f16 = IEEE binary16 stored as uint16_t):
+ *   q, out   [n_seq][q_tokens][n_head][hd]
+ *   k, v     cache rows of n_kv*hd values, row r at k + r*kv_row_stride;
+ *            key position j of sequence s lives in row
+ *            seq_kv_offset[s] + (ring_cap ? j % ring_cap : j)
+ *   sinks    [n_head] f32 logits (natural-log units) or NULL
+ *   partials [slot][n_head][hd + 2] f32 (max, sum, hd sums of v) — the
+ *            reference's merge_dec / cpu_attn partial format.
+ *
+ * Token t of sequence s is the query at position kv_len_s - q_tokens + t and
+ * sees keys [lo, pos] with lo = max(0, pos + 1 - window) when a window is
+ * set (causal among the pass's own tokens: drafts and prompt rows).
+ *
+ * The reference (HumandubleOfficial/Pelica) has no single attention function:
+ * each entry point below replaces a set of WGSL dispatches recorded by its
+ * engines, cited per function.
+ */
+#ifndef PELICA_ATTN_H
+#define PELICA_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PELICA_ATTN_VERSION 1
+
+/* status codes */
+#define PELICA_ATTN_OK 0
+#define PELICA_ATTN_EINVAL (-1)      /* bad descriptor or argument */
+#define PELICA_ATTN_EUNSUPPORTED (-2) /* valid but not implemented (e.g. hd) */
+#define PELICA_ATTN_EHIP (-3)        /* a HIP runtime call failed */
+#define PELICA_ATTN_EWORKSPACE (-4)  /* workspace missing or too small */
+
+/* Shape and addressing of one attention call.  Replaces the 16-word u32
+ * argument blocks of the reference's attention kernels
+ * (src/moe_kernels.rs:39-43 arg(), src/oss.rs:760-778 params; fields of
+ * src/cpu_attn.rs:13-26 Shape: hd, n_kv, hpk = n_head / n_kv). */
+typedef struct PelicaAttnDesc {
+    int32_t n_head;    /* query heads */
+    int32_t n_kv;      /* kv heads; n_head % n_kv == 0 (GQA group n_head/n_kv) */
+    int32_t hd;        /* dims per head: 64 or 128 */
+    int32_t n_seq;     /* sequences in the batch (>= 1) */
+    int32_t q_tokens;  /* query tokens per sequence: 1 decode, <= 8 drafts, T prompt */
+    int32_t kv_len;    /* keys per sequence; with seq_kv_len set, an upper bound */
+    const int32_t* seq_kv_len;    /* device [n_seq] keys per sequence, or NULL */
+    const int64_t* seq_kv_offset; /* device [n_seq] first cache row, or NULL:
+                                     sequence s then starts at row s * (ring_cap ? ring_cap : kv_len) */
+    int64_t kv_row_stride; /* f16 values between cache rows; 0 = n_kv * hd */
+    int32_t window;    /* sliding window in keys, 0 = all (src/oss_batch.rs:175) */
+    int32_t ring_cap;  /* 0 = linear cache; else rows of a ring of ring_cap positions
+                          (src/oss_batch.rs:205, src/oss.rs:570-572) */
+    float scale;       /* logit scale; 0 = 1/sqrt(hd) (src/moe.rs:1263) */
+    uint32_t flags;    /* reserved, must be 0 */
+} PelicaAttnDesc;
+
+/* PELICA_ATTN_VERSION of the loaded library. */
+int pelica_attn_version(void);
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char* pelica_attn_last_error(void);
+
+/* Bytes of device workspace pelica_attn_decode needs for this descriptor
+ * (split-K partials).  0 on an invalid descriptor (see last_error) or when
+ * the call needs none. */
+size_t pelica_attn_workspace_bytes(const PelicaAttnDesc* desc);
+
+/* Decode attention: f32 queries over the f16 cache, f32 output, split-K
+ * flash-decode plus an in-order combine with the sinks.
+ * Replaces: attn_dec / attn_dec_fast + merge_dec (src/moe_kernels.rs:482-808,
+ * dispatched at src/moe.rs:1343,1364), ATTN_T (src/oss_batch.rs:172-251,
+ * src/oss.rs:675-683), attn_s + ATTN_M (src/oss_batch.rs:253-425,
+ * src/oss.rs:685-693) and the draft-verify pass of those (T <= 8). */
+int pelica_attn_decode(const PelicaAttnDesc* desc, const float* q, const uint16_t* k,
+                       const uint16_t* v, const float* sinks, float* out,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/* Prefill (prompt) attention: f16 queries, f16 cache, f16 output, f32
+ * accumulation and softmax, causal with optional window and sinks.
+ * Replaces: attn_p (src/oss_prefill.rs:391-526, src/oss.rs:734-741) and
+ * attn_pre + attn_fold (src/moe_kernels.rs:810-990, src/moe.rs:1345-1362). */
+int pelica_attn_prefill(const PelicaAttnDesc* desc, const uint16_t* q, const uint16_t* k,
+                        const uint16_t* v, const float* sinks, uint16_t* out, void* stream);
+
+/* Combine n_parts partial slots of one decode token (parts[(c*n_head+h)*(hd+2)],
+ * natural-log max) in slot order, with optional sinks, into out[n_head][hd].
+ * Slots whose max is -3e38 (or -inf) carry no weight, as the reference's
+ * empty slots do.  Replaces merge_dec (src/moe_kernels.rs:585-617) and
+ * ATTN_M's combine (src/oss_batch.rs:395-425); it is how partials from the
+ * CPU tier (cpu_attn::chunk, src/moe.rs:1686-1729) join the GPU's. */
+int pelica_attn_partials_merge(int32_t n_head, int32_t hd, int32_t n_parts,
+                               const float* parts, const float* sinks, float* out,
+                               void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

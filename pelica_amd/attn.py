@@ -1,0 +1,250 @@
+"""Host binding of libpelica_attn.so (include/pelica_attn.h) for torch tensors.
+
+The reference has no single attention function: its engines record WGSL
+dispatches (src/moe.rs:1343,1364 decode; src/oss.rs:675-694 gpt-oss decode and
+drafts; src/oss.rs:734-741 prompt) and its CPU tier calls
+``cpu_attn::chunk(&Shape, kv, k, v, q, out)`` (src/cpu_attn.rs:72).  This
+module mirrors that surface: ``Shape`` is ``cpu_attn::Shape``
+(src/cpu_attn.rs:13-26), ``decode`` / ``prefill`` / ``partials_merge`` are the
+three C entry points.  Errors come back as ``AttnError`` carrying the C status
+and the library's message (the reference returns ``anyhow::Result`` from its
+engine calls).
+
+There is no CPU fallback: without the built library every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from dataclasses import dataclass
+from typing import Optional
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+
+OK = 0
+EINVAL = -1
+EUNSUPPORTED = -2
+EHIP = -3
+EWORKSPACE = -4
+
+#: every symbol include/pelica_attn.h declares
+EXPORTS = (
+    "pelica_attn_version",
+    "pelica_attn_last_error",
+    "pelica_attn_workspace_bytes",
+    "pelica_attn_decode",
+    "pelica_attn_prefill",
+    "pelica_attn_partials_merge",
+)
+
+
+class AttnError(RuntimeError):
+    """A failed libpelica_attn call: ``code`` is the C status."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"pelica_attn error {code}: {message}")
+        self.code = code
+        self.message = message
+
+
+@dataclass(frozen=True)
+class Shape:
+    """``cpu_attn::Shape``: dims per head, kv heads, query heads per kv head."""
+
+    hd: int
+    n_kv: int
+    hpk: int
+
+    def row(self) -> int:
+        """f16 values per cache row (one position's keys or values)."""
+        return self.n_kv * self.hd
+
+    @property
+    def n_head(self) -> int:
+        return self.n_kv * self.hpk
+
+
+class AttnDesc(ctypes.Structure):
+    """``PelicaAttnDesc`` (field meanings in include/pelica_attn.h)."""
+
+    _fields_ = [
+        ("n_head", ctypes.c_int32),
+        ("n_kv", ctypes.c_int32),
+        ("hd", ctypes.c_int32),
+        ("n_seq", ctypes.c_int32),
+        ("q_tokens", ctypes.c_int32),
+        ("kv_len", ctypes.c_int32),
+        ("seq_kv_len", ctypes.c_void_p),
+        ("seq_kv_offset", ctypes.c_void_p),
+        ("kv_row_stride", ctypes.c_int64),
+        ("window", ctypes.c_int32),
+        ("ring_cap", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("flags", ctypes.c_uint32),
+    ]
+
+
+_lib = None
+
+
+def library_path() -> str:
+    return os.environ.get("PELICA_ATTN_LIB", os.path.join(_HERE, "lib", "libpelica_attn.so"))
+
+
+def load_library() -> ctypes.CDLL:
+    """Load libpelica_attn.so once.  Raises when it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = library_path()
+    if not os.path.exists(path):
+        raise AttnError(EHIP, f"{path} is not built (run __graft_entry__.build() or make -C pelica_amd/csrc)")
+    try:  # the HIP runtime torch ships must be the one the library binds to
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+    lib = ctypes.CDLL(path)
+    vp, i32, sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_size_t
+    dp = ctypes.POINTER(AttnDesc)
+    lib.pelica_attn_version.restype = ctypes.c_int
+    lib.pelica_attn_version.argtypes = []
+    lib.pelica_attn_last_error.restype = ctypes.c_char_p
+    lib.pelica_attn_last_error.argtypes = []
+    lib.pelica_attn_workspace_bytes.restype = sz
+    lib.pelica_attn_workspace_bytes.argtypes = [dp]
+    lib.pelica_attn_decode.restype = ctypes.c_int
+    lib.pelica_attn_decode.argtypes = [dp, vp, vp, vp, vp, vp, vp, sz, vp]
+    lib.pelica_attn_prefill.restype = ctypes.c_int
+    lib.pelica_attn_prefill.argtypes = [dp, vp, vp, vp, vp, vp, vp]
+    lib.pelica_attn_partials_merge.restype = ctypes.c_int
+    lib.pelica_attn_partials_merge.argtypes = [i32, i32, i32, vp, vp, vp, vp]
+    _lib = lib
+    return lib
+
+
+def _check(rc: int) -> None:
+    if rc != OK:
+        msg = load_library().pelica_attn_last_error().decode(errors="replace")
+        raise AttnError(rc, msg)
+
+
+def _ptr(t) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream_ptr(stream) -> Optional[int]:
+    import torch
+
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream or None
+
+
+def make_desc(n_head: int, n_kv: int, hd: int, *, n_seq: int = 1, q_tokens: int = 1, kv_len: int,
+              seq_kv_len=None, seq_kv_offset=None, kv_row_stride: int = 0, window: int = 0,
+              ring_cap: int = 0, scale: Optional[float] = None) -> AttnDesc:
+    d = AttnDesc()
+    d.n_head, d.n_kv, d.hd = n_head, n_kv, hd
+    d.n_seq, d.q_tokens, d.kv_len = n_seq, q_tokens, kv_len
+    d.seq_kv_len = _ptr(seq_kv_len)
+    d.seq_kv_offset = _ptr(seq_kv_offset)
+    d.kv_row_stride = kv_row_stride
+    d.window, d.ring_cap = window, ring_cap
+    d.scale = 0.0 if scale is None else float(scale)
+    d.flags = 0
+    return d
+
+
+def _validate_lens(seq_kv_len, seq_kv_offset):
+    import torch
+
+    if seq_kv_len is not None:
+        assert seq_kv_len.dtype == torch.int32 and seq_kv_len.is_cuda and seq_kv_len.is_contiguous()
+    if seq_kv_offset is not None:
+        assert seq_kv_offset.dtype == torch.int64 and seq_kv_offset.is_cuda and seq_kv_offset.is_contiguous()
+
+
+def workspace_bytes(desc: AttnDesc) -> int:
+    n = load_library().pelica_attn_workspace_bytes(ctypes.byref(desc))
+    if n == 0:
+        msg = load_library().pelica_attn_last_error().decode(errors="replace")
+        if msg:
+            raise AttnError(EINVAL, msg)
+    return n
+
+
+def decode(q, k, v, *, n_kv: int, kv_len: int, sinks=None, window: int = 0, ring_cap: int = 0,
+           scale: Optional[float] = None, seq_kv_len=None, seq_kv_offset=None, kv_row_stride: int = 0,
+           out=None, workspace=None, stream=None):
+    """Decode attention.  q: f32 [n_seq, q_tokens, n_head, hd] (CUDA);
+    k, v: f16 cache rows (any shape, contiguous); returns f32 like q."""
+    import torch
+
+    assert q.dtype == torch.float32 and q.dim() == 4 and q.is_contiguous() and q.is_cuda
+    assert k.dtype == torch.float16 and v.dtype == torch.float16 and k.is_contiguous() and v.is_contiguous()
+    _validate_lens(seq_kv_len, seq_kv_offset)
+    n_seq, T, n_head, hd = q.shape
+    desc = make_desc(n_head, n_kv, hd, n_seq=n_seq, q_tokens=T, kv_len=kv_len, seq_kv_len=seq_kv_len,
+                     seq_kv_offset=seq_kv_offset, kv_row_stride=kv_row_stride, window=window,
+                     ring_cap=ring_cap, scale=scale)
+    lib = load_library()
+    need = lib.pelica_attn_workspace_bytes(ctypes.byref(desc))
+    if need == 0:
+        msg = lib.pelica_attn_last_error().decode(errors="replace")
+        if msg:
+            raise AttnError(EINVAL, msg)
+    if out is None:
+        out = torch.empty_like(q)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    if sinks is not None:
+        assert sinks.dtype == torch.float32 and sinks.is_cuda and sinks.numel() == n_head
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _check(lib.pelica_attn_decode(ctypes.byref(desc), _ptr(q), _ptr(k), _ptr(v), _ptr(sinks), _ptr(out),
+                                  _ptr(workspace), ws_bytes, _stream_ptr(stream)))
+    return out
+
+
+def prefill(q, k, v, *, n_kv: int, kv_len: Optional[int] = None, sinks=None, window: int = 0,
+            ring_cap: int = 0, scale: Optional[float] = None, seq_kv_len=None, seq_kv_offset=None,
+            kv_row_stride: int = 0, out=None, stream=None):
+    """Prompt attention.  q: f16 [n_seq, T, n_head, hd]; k, v: f16 cache rows;
+    kv_len defaults to T (a prompt that starts the cache).  Returns f16."""
+    import torch
+
+    assert q.dtype == torch.float16 and q.dim() == 4 and q.is_contiguous() and q.is_cuda
+    assert k.dtype == torch.float16 and v.dtype == torch.float16 and k.is_contiguous() and v.is_contiguous()
+    _validate_lens(seq_kv_len, seq_kv_offset)
+    n_seq, T, n_head, hd = q.shape
+    desc = make_desc(n_head, n_kv, hd, n_seq=n_seq, q_tokens=T, kv_len=T if kv_len is None else kv_len,
+                     seq_kv_len=seq_kv_len, seq_kv_offset=seq_kv_offset, kv_row_stride=kv_row_stride,
+                     window=window, ring_cap=ring_cap, scale=scale)
+    if out is None:
+        out = torch.empty_like(q)
+    if sinks is not None:
+        assert sinks.dtype == torch.float32 and sinks.is_cuda and sinks.numel() == n_head
+    lib = load_library()
+    _check(lib.pelica_attn_prefill(ctypes.byref(desc), _ptr(q), _ptr(k), _ptr(v), _ptr(sinks), _ptr(out),
+                                   _stream_ptr(stream)))
+    return out
+
+
+def partials_merge(parts, *, n_head: int, hd: int, sinks=None, out=None, stream=None):
+    """Combine partial slots [n_parts, n_head, hd + 2] (max, sum, O) in slot
+    order with optional sinks into f32 [n_head, hd]."""
+    import torch
+
+    assert parts.dtype == torch.float32 and parts.is_cuda and parts.is_contiguous()
+    n_parts = parts.numel() // (n_head * (hd + 2))
+    assert n_parts * n_head * (hd + 2) == parts.numel()
+    if out is None:
+        out = torch.empty(n_head, hd, dtype=torch.float32, device=parts.device)
+    lib = load_library()
+    _check(lib.pelica_attn_partials_merge(n_head, hd, n_parts, _ptr(parts), _ptr(sinks), _ptr(out),
+                                          _stream_ptr(stream)))
+    return out
+
+
+def default_scale(hd: int) -> float:
+    return 1.0 / math.sqrt(hd)

@@ -1,0 +1,237 @@
+// The C ABI of libpelica_attn.so (include/pelica_attn.h): descriptor
+// validation, split planning, launches, and the partials merge kernel.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+
+#include "../../include/pelica_attn.h"
+#include "attn_decode.hpp"
+#include "attn_prefill.hpp"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int env_int(const char* name, int dflt) {
+    const char* s = getenv(name);
+    if (!s || !*s) return dflt;
+    return atoi(s);
+}
+
+bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) != 0; }
+
+int ceil_div(long long a, long long b) { return (int)((a + b - 1) / b); }
+
+// Checks shared by decode and prefill.
+int check_desc(const PelicaAttnDesc* d) {
+    if (!d) return fail(PELICA_ATTN_EINVAL, "desc is NULL");
+    if (d->flags != 0) return fail(PELICA_ATTN_EINVAL, "flags must be 0 (got %u)", d->flags);
+    if (d->n_head <= 0 || d->n_kv <= 0 || d->n_head % d->n_kv)
+        return fail(PELICA_ATTN_EINVAL, "n_head %d must be a positive multiple of n_kv %d", d->n_head, d->n_kv);
+    if (d->hd != 64 && d->hd != 128)
+        return fail(PELICA_ATTN_EUNSUPPORTED, "hd %d unsupported (64 or 128)", d->hd);
+    if (d->n_seq <= 0 || d->q_tokens <= 0)
+        return fail(PELICA_ATTN_EINVAL, "n_seq %d and q_tokens %d must be positive", d->n_seq, d->q_tokens);
+    if (d->kv_len < d->q_tokens)
+        return fail(PELICA_ATTN_EINVAL, "kv_len %d is below q_tokens %d (the queries' own keys are in the cache)",
+                    d->kv_len, d->q_tokens);
+    if (d->window < 0 || d->ring_cap < 0)
+        return fail(PELICA_ATTN_EINVAL, "window %d and ring_cap %d must be >= 0", d->window, d->ring_cap);
+    if (d->kv_row_stride != 0 && d->kv_row_stride < (int64_t)d->n_kv * d->hd)
+        return fail(PELICA_ATTN_EINVAL, "kv_row_stride %lld is below n_kv*hd", (long long)d->kv_row_stride);
+    if (d->kv_row_stride % 8)
+        return fail(PELICA_ATTN_EINVAL, "kv_row_stride must be a multiple of 8 values (16-byte rows)");
+    if (d->ring_cap) {
+        // every key a token of the pass sees must still be in the ring
+        const int pos0 = d->kv_len - d->q_tokens;
+        const int lo0 = (d->window > 0 && pos0 + 1 > d->window) ? pos0 + 1 - d->window : 0;
+        if (d->kv_len - lo0 > d->ring_cap)
+            return fail(PELICA_ATTN_EINVAL, "ring_cap %d cannot hold the %d keys the pass sees", d->ring_cap,
+                        d->kv_len - lo0);
+    }
+    if (!(d->scale >= 0.f) || std::isinf(d->scale)) return fail(PELICA_ATTN_EINVAL, "scale must be finite, >= 0");
+    return PELICA_ATTN_OK;
+}
+
+float eff_scale(const PelicaAttnDesc* d) { return d->scale > 0.f ? d->scale : 1.f / std::sqrt((float)d->hd); }
+
+struct DecodePlan {
+    int R, rt, n_rg, split_keys, n_slot;
+    size_t ws_bytes;
+};
+
+int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
+    int rc = check_desc(d);
+    if (rc) return rc;
+    const int hpk = d->n_head / d->n_kv;
+    const int R = d->q_tokens * hpk;
+    int rt;
+    if (d->hd == 64) rt = R <= 16 ? 1 : R <= 32 ? 2 : 4;
+    else rt = R <= 16 ? 1 : 2;
+    const int n_rg = ceil_div(R, 16 * rt);
+    // keys any row of a sequence can see
+    const long long span = d->window > 0 ? std::min<long long>(d->kv_len, (long long)d->window + d->q_tokens - 1)
+                                         : d->kv_len;
+    const long long blocks = ceil_div(span, 64);
+    const long long rows_of_work = (long long)d->n_seq * d->n_kv * n_rg;
+    const int target = env_int("PELICA_ATTN_DECODE_WGS", 1024);
+    int sb = env_int("PELICA_ATTN_SPLIT_BLOCKS", 0);
+    if (sb <= 0) sb = std::max<long long>(1, (blocks * rows_of_work + target - 1) / std::max(1, target));
+    int split_keys = 64 * sb, n_slot = 0;
+    for (;;) {
+        const int total = ceil_div(d->kv_len, split_keys);
+        n_slot = d->window > 0 ? std::min<int>(total, ceil_div(span, split_keys) + 1) : total;
+        if (n_slot <= pelica::kMaxSlots) break;
+        split_keys *= 2;
+    }
+    pl->R = R;
+    pl->rt = rt;
+    pl->n_rg = n_rg;
+    pl->split_keys = split_keys;
+    pl->n_slot = n_slot;
+    // (max, sum) pairs, then O rows 16-byte aligned
+    const size_t n_part = (size_t)d->n_seq * d->n_kv * R * n_slot;
+    pl->ws_bytes = n_slot > 1 ? (((2 * n_part + 3) & ~(size_t)3) + n_part * d->hd) * sizeof(float) : 0;
+    return PELICA_ATTN_OK;
+}
+
+// merge of externally produced partials, natural-log max (merge_dec format)
+__global__ __launch_bounds__(64) void partials_merge_kernel(int n_head, int hd, int n_parts, const float* parts,
+                                                            const float* sinks, float* out) {
+    const int h = blockIdx.x, lane = threadIdx.x;
+    const size_t stride = (size_t)n_head * (hd + 2);
+    const float* ph = parts + (size_t)h * (hd + 2);
+    const float sk = sinks ? sinks[h] : -INFINITY;
+    float M = sk;
+    for (int c = lane; c < n_parts; c += 64) M = fmaxf(M, ph[c * stride]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    const float ms = (M == -INFINITY) ? 0.f : M;
+    float L = 0.f;
+    for (int c = lane; c < n_parts; c += 64) L += ph[c * stride + 1] * pelica::fast_exp2((ph[c * stride] - ms) * pelica::kLog2e);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off, 64);
+    if (sinks) L += pelica::fast_exp2((sk - ms) * pelica::kLog2e);
+    const float inv = 1.f / L;
+    for (int d = lane; d < hd; d += 64) {
+        float acc = 0.f;
+        for (int c = 0; c < n_parts; ++c)
+            acc += ph[c * stride + 2 + d] * pelica::fast_exp2((ph[c * stride] - ms) * pelica::kLog2e);
+        out[(size_t)h * hd + d] = acc * inv;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int pelica_attn_version(void) { return PELICA_ATTN_VERSION; }
+
+const char* pelica_attn_last_error(void) { return g_err; }
+
+size_t pelica_attn_workspace_bytes(const PelicaAttnDesc* desc) {
+    g_err[0] = 0;
+    DecodePlan pl;
+    if (plan_decode(desc, &pl)) return 0;
+    return pl.ws_bytes;
+}
+
+int pelica_attn_decode(const PelicaAttnDesc* desc, const float* q, const uint16_t* k, const uint16_t* v,
+                       const float* sinks, float* out, void* workspace, size_t workspace_bytes, void* stream) {
+    g_err[0] = 0;
+    DecodePlan pl;
+    int rc = plan_decode(desc, &pl);
+    if (rc) return rc;
+    if (!q || !k || !v || !out) return fail(PELICA_ATTN_EINVAL, "q, k, v and out must be non-NULL");
+    if (misaligned(q) || misaligned(k) || misaligned(v) || misaligned(out) || misaligned(workspace))
+        return fail(PELICA_ATTN_EINVAL, "q, k, v, out and workspace must be 16-byte aligned");
+    if (pl.ws_bytes && (!workspace || workspace_bytes < pl.ws_bytes))
+        return fail(PELICA_ATTN_EWORKSPACE, "workspace of %zu bytes needed, %zu given", pl.ws_bytes,
+                    workspace ? workspace_bytes : (size_t)0);
+    pelica::DecodeParams p{};
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.sinks = sinks;
+    p.out = out;
+    const size_t n_part = (size_t)desc->n_seq * desc->n_kv * pl.R * pl.n_slot;
+    p.ws_ml = pl.ws_bytes ? static_cast<float*>(workspace) : nullptr;
+    p.ws_o = pl.ws_bytes ? static_cast<float*>(workspace) + ((2 * n_part + 3) & ~(size_t)3) : nullptr;
+    p.seq_len = desc->seq_kv_len;
+    p.seq_off = desc->seq_kv_offset;
+    p.row_stride = desc->kv_row_stride ? desc->kv_row_stride : (int64_t)desc->n_kv * desc->hd;
+    p.kv_len = desc->kv_len;
+    p.n_head = desc->n_head;
+    p.n_kv = desc->n_kv;
+    p.hd = desc->hd;
+    p.hpk = desc->n_head / desc->n_kv;
+    p.T = desc->q_tokens;
+    p.R = pl.R;
+    p.n_seq = desc->n_seq;
+    p.window = desc->window;
+    p.ring_cap = desc->ring_cap;
+    p.qscale = eff_scale(desc) * pelica::kLog2e;
+    p.n_slot = pl.n_slot;
+    p.split_keys = pl.split_keys;
+    hipError_t e = pelica::launch_decode(p, pl.rt, pl.n_rg, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(PELICA_ATTN_EHIP, "decode launch: %s", hipGetErrorString(e));
+    return PELICA_ATTN_OK;
+}
+
+int pelica_attn_prefill(const PelicaAttnDesc* desc, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                        const float* sinks, uint16_t* out, void* stream) {
+    g_err[0] = 0;
+    int rc = check_desc(desc);
+    if (rc) return rc;
+    if (!q || !k || !v || !out) return fail(PELICA_ATTN_EINVAL, "q, k, v and out must be non-NULL");
+    if (misaligned(q) || misaligned(k) || misaligned(v) || misaligned(out))
+        return fail(PELICA_ATTN_EINVAL, "q, k, v and out must be 16-byte aligned");
+    pelica::PrefillParams p{};
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.sinks = sinks;
+    p.out = out;
+    p.seq_len = desc->seq_kv_len;
+    p.seq_off = desc->seq_kv_offset;
+    p.row_stride = desc->kv_row_stride ? desc->kv_row_stride : (int64_t)desc->n_kv * desc->hd;
+    p.kv_len = desc->kv_len;
+    p.n_head = desc->n_head;
+    p.n_kv = desc->n_kv;
+    p.hd = desc->hd;
+    p.hpk = desc->n_head / desc->n_kv;
+    p.T = desc->q_tokens;
+    p.n_seq = desc->n_seq;
+    p.window = desc->window;
+    p.ring_cap = desc->ring_cap;
+    p.qscale = eff_scale(desc) * pelica::kLog2e;
+    hipError_t e = pelica::launch_prefill(p, static_cast<hipStream_t>(stream));
+    if (e == hipErrorNotSupported) return fail(PELICA_ATTN_EUNSUPPORTED, "prefill shape unsupported");
+    if (e != hipSuccess) return fail(PELICA_ATTN_EHIP, "prefill launch: %s", hipGetErrorString(e));
+    return PELICA_ATTN_OK;
+}
+
+int pelica_attn_partials_merge(int32_t n_head, int32_t hd, int32_t n_parts, const float* parts, const float* sinks,
+                               float* out, void* stream) {
+    g_err[0] = 0;
+    if (n_head <= 0 || hd <= 0 || n_parts <= 0)
+        return fail(PELICA_ATTN_EINVAL, "n_head %d, hd %d and n_parts %d must be positive", n_head, hd, n_parts);
+    if (!parts || !out) return fail(PELICA_ATTN_EINVAL, "parts and out must be non-NULL");
+    hipLaunchKernelGGL(partials_merge_kernel, dim3(n_head), dim3(64), 0, static_cast<hipStream_t>(stream), n_head, hd,
+                       n_parts, parts, sinks, out);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(PELICA_ATTN_EHIP, "merge launch: %s", hipGetErrorString(e));
+    return PELICA_ATTN_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,30 @@
+// Launch parameters of the decode kernels (attn_decode.hip).
+#pragma once
+#include "attn_common.hpp"
+
+namespace pelica {
+
+// most key splits one row can have (combine stages one weight per split in LDS)
+constexpr int kMaxSlots = 4096;
+
+struct DecodeParams {
+    const float* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    const float* sinks;
+    float* out;
+    float* ws_ml;  // [n_seq][n_kv][R][n_slot] x (max, sum), base-2 max
+    float* ws_o;   // [n_seq][n_kv][R][n_slot][hd]
+    const int32_t* seq_len;
+    const int64_t* seq_off;
+    int64_t row_stride;  // f16 values between cache rows
+    int kv_len, n_head, n_kv, hd, hpk, T, R, n_seq;
+    int window, ring_cap;
+    float qscale;        // scale * log2(e)
+    int n_slot;          // key splits per (sequence, kv head) in the grid
+    int split_keys;      // keys per split, a multiple of 64
+};
+
+hipError_t launch_decode(const DecodeParams& p, int rt, int n_rg, hipStream_t st);
+
+}  // namespace pelica

@@ -1,0 +1,24 @@
+// Launch parameters of the prefill kernel (attn_prefill.hip).
+#pragma once
+#include "attn_common.hpp"
+
+namespace pelica {
+
+struct PrefillParams {
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    const float* sinks;
+    uint16_t* out;
+    const int32_t* seq_len;
+    const int64_t* seq_off;
+    int64_t row_stride;  // f16 values between cache rows
+    int kv_len, n_head, n_kv, hd, hpk, T, n_seq;
+    int window, ring_cap;
+    float qscale;  // scale * log2(e)
+};
+
+// hipErrorNotSupported for shapes the kernel does not take
+hipError_t launch_prefill(const PrefillParams& p, hipStream_t st);
+
+}  // namespace pelica

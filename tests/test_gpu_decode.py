@@ -1,0 +1,139 @@
+"""GPU parity of pelica_attn_decode (and the partials merge) against the CPU
+oracle on identical seeded inputs, through the C ABI.
+
+Tolerance (north star): max |gpu - oracle| <= 2e-3 and
+||gpu - oracle||_2 / ||oracle||_2 <= 1e-3, fp32 output.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from pelica_amd import attn
+from pelica_amd import workloads as wl
+from tests.gpu_util import as_f64, gpu_run, oracle_run, to_np_f16
+from tests.refimpl import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def check(inp, what, **kw):
+    print(f"[case] {what}", flush=True)
+    got = gpu_run(inp, **kw)
+    ref = oracle_run(inp, **kw)
+    return assert_close(as_f64(got), as_f64(ref), what=what)
+
+
+@pytest.mark.parametrize("cfg", [wl.C1, wl.C2, wl.C3_FULL, wl.C3_SWA, wl.C5], ids=lambda c: c.name)
+def test_baseline_configs_full_size(cfg):
+    inp = wl.make_inputs(cfg, "cuda")
+    max_abs, rel = check(inp, cfg.name)
+    print(f"{cfg.name}: max_abs {max_abs:.2e} rel {rel:.2e}")
+
+
+@pytest.mark.parametrize("hd,n_head,n_kv", [(64, 64, 8), (128, 32, 4), (64, 16, 16), (128, 16, 16)])
+@pytest.mark.parametrize("kv_len", [1, 63, 65, 257, 1000, 4099])
+def test_lengths(hd, n_head, n_kv, kv_len):
+    cfg = wl.AttnConfig("len", "decode", n_head, n_kv, hd, kv_len, sinks=hd == 64, seed=kv_len)
+    check(wl.make_inputs(cfg, "cuda"), f"hd{hd} h{n_head}/{n_kv} len{kv_len}")
+
+
+@pytest.mark.parametrize("T", [2, 3, 4, 8])
+@pytest.mark.parametrize("hd,n_head,n_kv", [(64, 64, 8), (128, 32, 4), (128, 16, 16)])
+def test_draft_tokens(T, hd, n_head, n_kv):
+    cfg = wl.AttnConfig("drafts", "decode", n_head, n_kv, hd, 777, q_tokens=T, sinks=True, seed=T)
+    check(wl.make_inputs(cfg, "cuda"), f"T{T} hd{hd} h{n_head}/{n_kv}")
+
+
+@pytest.mark.parametrize("window", [1, 5, 128, 2000])
+@pytest.mark.parametrize("T", [1, 4])
+def test_windows(window, T):
+    cfg = wl.AttnConfig("win", "decode", 64, 8, 64, 1500, q_tokens=T, window=window, sinks=True, seed=window)
+    check(wl.make_inputs(cfg, "cuda"), f"window {window} T{T}")
+
+
+def test_ragged_batch_with_minimum_lengths():
+    cfg = wl.AttnConfig("ragged", "decode", 32, 4, 128, 3000, q_tokens=4, n_seq=6, ragged=(4, 3000), seed=9)
+    inp = wl.make_inputs(cfg, "cuda")
+    lens = inp.seq_len.clone()
+    lens[0] = 4          # only the drafts themselves
+    lens[1] = 5
+    inp.seq_len.copy_(lens)
+    check(inp, "ragged minimum lengths")
+
+
+def test_batch_without_offsets():
+    cfg = wl.AttnConfig("batch", "decode", 16, 4, 64, 700, n_seq=3, seed=21)
+    check(wl.make_inputs(cfg, "cuda"), "n_seq 3, default offsets")
+
+
+def test_ring_buffer_window_layer():
+    # the window layer's ring (src/oss.rs:570-572): position j in row j % cap
+    cap, L, T, W = 160, 5000, 3, 128
+    cfg = wl.AttnConfig("ring", "decode", 64, 8, 64, L, q_tokens=T, window=W, sinks=True, seed=33)
+    inp = wl.make_inputs(cfg, "cuda")
+    kr = torch.zeros(cap, 8, 64, dtype=torch.float16, device="cuda")
+    vr = torch.zeros_like(kr)
+    idx = torch.arange(L - cap, L, device="cuda")
+    kr[idx % cap] = inp.k[idx]
+    vr[idx % cap] = inp.v[idx]
+    got = gpu_run(inp, ring_cap=cap, k=kr, v=vr)
+    ref = oracle_run(inp)  # linear cache, same keys
+    assert_close(as_f64(got), as_f64(ref), what="ring")
+
+
+def test_padded_row_stride():
+    cfg = wl.AttnConfig("stride", "decode", 32, 4, 128, 900, sinks=True, seed=44)
+    inp = wl.make_inputs(cfg, "cuda")
+    stride = 4 * 128 + 64
+    kp = torch.zeros(900, stride, dtype=torch.float16, device="cuda")
+    vp = torch.zeros_like(kp)
+    kp[:, :512] = inp.k.reshape(900, 512)
+    vp[:, :512] = inp.v.reshape(900, 512)
+    got = gpu_run(inp, k=kp, v=vp, kv_row_stride=stride)
+    ref = oracle_run(inp)
+    assert_close(as_f64(got), as_f64(ref), what="row stride")
+
+
+def test_split_count_invariance(monkeypatch):
+    # the result does not depend on how the keys are split (fixed-order merge)
+    inp = wl.make_inputs(wl.C3_FULL.scaled(kv_len=9000), "cuda")
+    outs = []
+    for sb in ("1", "3", "16", "200"):
+        monkeypatch.setenv("PELICA_ATTN_SPLIT_BLOCKS", sb)
+        outs.append(as_f64(gpu_run(inp)))
+    for o in outs[1:]:
+        assert np.abs(o - outs[0]).max() < 2e-6
+
+
+def test_output_is_deterministic():
+    inp = wl.make_inputs(wl.C5, "cuda")
+    a = gpu_run(inp)
+    b = gpu_run(inp)
+    assert torch.equal(a, b)
+
+
+def test_partials_merge_joins_cpu_tier():
+    # the CPU tier's chunk partials (cpu_attn format) merged on the GPU with
+    # the sinks give the full attention (src/moe.rs:1713-1729)
+    cfg = wl.AttnConfig("merge", "decode", 32, 4, 128, 2000, sinks=True, seed=55)
+    inp = wl.make_inputs(cfg, "cuda")
+    q = inp.q.cpu().numpy()
+    parts = orc.partials(q, to_np_f16(inp.k), to_np_f16(inp.v), n_kv=4, kv_len=2000)
+    # pad with empty slots the way cpu_layer does (max -3e38)
+    empty = np.zeros((3, 32, 130), np.float32)
+    empty[:, :, 0] = -3e38
+    parts = np.concatenate([parts[:2], empty, parts[2:]])
+    out = attn.partials_merge(torch.from_numpy(parts).cuda(), n_head=32, hd=128, sinks=inp.sinks)
+    torch.cuda.synchronize()
+    ref = oracle_run(inp)
+    assert_close(as_f64(out), as_f64(ref)[0, 0], what="partials merge")
+
+
+def test_errors_surface_as_exceptions():
+    inp = wl.make_inputs(wl.C3_FULL.scaled(kv_len=128), "cuda")
+    with pytest.raises(attn.AttnError) as e:
+        attn.decode(inp.q, inp.k, inp.v, n_kv=8, kv_len=128, window=-3)
+    assert e.value.code == attn.EINVAL

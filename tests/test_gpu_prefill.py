@@ -1,0 +1,92 @@
+"""GPU parity of pelica_attn_prefill against the CPU oracle (f16 in/out, f32
+softmax and accumulation) on identical seeded inputs, through the C ABI.
+
+Both sides round the output to f16, so besides the 2e-3 / 1e-3 contract the
+residual is about one f16 ulp of the output.
+"""
+import numpy as np
+import pytest
+import torch
+
+from pelica_amd import workloads as wl
+from tests.gpu_util import as_f64, gpu_run, oracle_run
+from tests.refimpl import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def test_c4_full_causal_sampled_rows():
+    inp = wl.make_inputs(wl.C4_FULL, "cuda")
+    print("[case] c4 full", flush=True)
+    got = as_f64(gpu_run(inp))
+    for t0, t1 in ((0, 96), (1000, 1040), (2047, 2112), (4000, 4096)):
+        ref = as_f64(oracle_run(inp, t_begin=t0, t_end=t1))
+        assert_close(got[:, t0:t1], ref[:, t0:t1], what=f"c4 full tokens {t0}..{t1}")
+    assert np.isfinite(got).all()
+
+
+def test_c4_window_all_rows():
+    inp = wl.make_inputs(wl.C4_SWA, "cuda")
+    print("[case] c4 swa", flush=True)
+    got = as_f64(gpu_run(inp))
+    ref = as_f64(oracle_run(inp))
+    assert_close(got, ref, what="c4 window 128")
+
+
+@pytest.mark.parametrize("T", [1, 7, 33, 64, 100, 257])
+@pytest.mark.parametrize("hd,n_head,n_kv", [(64, 64, 8), (128, 32, 4), (64, 8, 8), (128, 16, 1)])
+def test_small_prompts(T, hd, n_head, n_kv):
+    cfg = wl.AttnConfig("p", "prefill", n_head, n_kv, hd, T, q_tokens=T, sinks=(T % 2 == 1), seed=T + hd)
+    inp = wl.make_inputs(cfg, "cuda")
+    print(f"[case] prefill T{T} hd{hd} h{n_head}/{n_kv}", flush=True)
+    assert_close(as_f64(gpu_run(inp)), as_f64(oracle_run(inp)), what=f"T{T} hd{hd}")
+
+
+@pytest.mark.parametrize("window", [1, 17, 64, 128, 1000])
+def test_windows(window):
+    cfg = wl.AttnConfig("pw", "prefill", 64, 8, 64, 700, q_tokens=700, window=window, sinks=True, seed=window)
+    inp = wl.make_inputs(cfg, "cuda")
+    print(f"[case] prefill window {window}", flush=True)
+    assert_close(as_f64(gpu_run(inp)), as_f64(oracle_run(inp)), what=f"window {window}")
+
+
+def test_prompt_after_cached_prefix():
+    # a second prompt chunk: 300 new tokens after 900 cached positions
+    cfg = wl.AttnConfig("chunk", "prefill", 64, 8, 64, 1200, q_tokens=300, sinks=True, seed=71)
+    inp = wl.make_inputs(cfg, "cuda")
+    print("[case] prefill after prefix", flush=True)
+    assert_close(as_f64(gpu_run(inp)), as_f64(oracle_run(inp)), what="prefix")
+
+
+def test_ragged_sequences():
+    cfg = wl.AttnConfig("pr", "prefill", 32, 4, 128, 600, q_tokens=64, n_seq=3, ragged=(64, 600), seed=72)
+    inp = wl.make_inputs(cfg, "cuda")
+    print("[case] prefill ragged", flush=True)
+    assert_close(as_f64(gpu_run(inp)), as_f64(oracle_run(inp)), what="ragged")
+
+
+def test_ring_window_prefill():
+    cap, L, T, W = 128 + 512, 3000, 512, 128
+    cfg = wl.AttnConfig("pring", "prefill", 64, 8, 64, L, q_tokens=T, window=W, sinks=True, seed=73)
+    inp = wl.make_inputs(cfg, "cuda")
+    kr = torch.zeros(cap, 8, 64, dtype=torch.float16, device="cuda")
+    vr = torch.zeros_like(kr)
+    idx = torch.arange(L - cap, L, device="cuda")
+    kr[idx % cap] = inp.k[idx]
+    vr[idx % cap] = inp.v[idx]
+    print("[case] prefill ring", flush=True)
+    got = gpu_run(inp, ring_cap=cap, k=kr, v=vr)
+    assert_close(as_f64(got), as_f64(oracle_run(inp)), what="prefill ring")
+
+
+def test_prefill_matches_decode_rows():
+    # the prompt's last row equals a one-token decode at that position
+    # (f32 queries rounded the same way), within the f16 output rounding
+    cfg = wl.AttnConfig("pd", "prefill", 64, 8, 64, 500, q_tokens=500, sinks=True, seed=74)
+    inp = wl.make_inputs(cfg, "cuda")
+    from pelica_amd import attn
+
+    pre = gpu_run(inp)
+    dec = attn.decode(inp.q[:, -1:].float().contiguous(), inp.k, inp.v, n_kv=8, kv_len=500, sinks=inp.sinks)
+    torch.cuda.synchronize()
+    assert_close(as_f64(pre[:, -1:]), as_f64(dec), atol=2e-3, rtol=1e-3, what="prefill vs decode")

@@ -1,0 +1,106 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports what
+include/pelica_attn.h declares, descriptors are validated with the documented
+status codes, and the workload byte/flop counts match BASELINE's figures."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from pelica_amd import attn
+from pelica_amd import workloads as wl
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    text = open(os.path.join(ROOT, "include", "pelica_attn.h")).read()
+    return sorted(set(re.findall(r"\b(pelica_attn_\w+)\s*\(", text)))
+
+
+def test_header_matches_binding_list():
+    assert header_functions() == sorted(attn.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = attn.load_library()
+    for name in header_functions():
+        assert hasattr(lib, name), name
+    assert lib.pelica_attn_version() == 1
+
+
+def _desc(**kw):
+    base = dict(n_head=64, n_kv=8, hd=64, n_seq=1, q_tokens=1, kv_len=32768)
+    base.update(kw)
+    n_head, n_kv, hd = base.pop("n_head"), base.pop("n_kv"), base.pop("hd")
+    return attn.make_desc(n_head, n_kv, hd, **base)
+
+
+def test_workspace_sizes():
+    # gpt-oss decode: 8 kv heads x 8 rows x splits x (2 + 64) floats
+    n = attn.workspace_bytes(_desc())
+    assert n > 0 and n % 4 == 0
+    # a single split needs no workspace
+    assert attn.workspace_bytes(_desc(kv_len=64, n_kv=64, n_head=64)) == 0
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(hd=96), attn.EUNSUPPORTED),
+    (dict(n_head=60), attn.EINVAL),
+    (dict(kv_len=0), attn.EINVAL),
+    (dict(q_tokens=4, kv_len=3), attn.EINVAL),
+    (dict(window=-1), attn.EINVAL),
+    (dict(ring_cap=100, window=0, kv_len=1000), attn.EINVAL),
+    (dict(kv_row_stride=12), attn.EINVAL),
+])
+def test_invalid_descriptors(kw, code):
+    lib = attn.load_library()
+    d = _desc(**kw)
+    assert lib.pelica_attn_workspace_bytes(ctypes.byref(d)) == 0
+    msg = lib.pelica_attn_last_error().decode()
+    assert msg, kw
+    # the decode entry point reports the same status before touching the GPU
+    rc = lib.pelica_attn_decode(ctypes.byref(d), 16, 16, 16, None, 16, None, 0, None)
+    assert rc == code, (kw, rc, lib.pelica_attn_last_error())
+
+
+def test_null_and_misaligned_pointers():
+    lib = attn.load_library()
+    d = _desc(kv_len=64, n_kv=64)
+    assert lib.pelica_attn_decode(ctypes.byref(d), None, 16, 16, None, 16, None, 0, None) == attn.EINVAL
+    assert lib.pelica_attn_decode(ctypes.byref(d), 8, 16, 16, None, 16, None, 0, None) == attn.EINVAL
+    assert b"aligned" in lib.pelica_attn_last_error()
+    assert lib.pelica_attn_prefill(ctypes.byref(d), 16, None, 16, None, 16, None) == attn.EINVAL
+    assert lib.pelica_attn_partials_merge(0, 64, 1, 16, None, 16, None) == attn.EINVAL
+
+
+def test_workspace_too_small_is_reported():
+    lib = attn.load_library()
+    d = _desc()
+    need = lib.pelica_attn_workspace_bytes(ctypes.byref(d))
+    rc = lib.pelica_attn_decode(ctypes.byref(d), 16, 16, 16, None, 16, 16, need - 16, None)
+    assert rc == attn.EWORKSPACE
+
+
+def test_baseline_work_counts():
+    # BASELINE.md section 2 figures
+    assert wl.kv_bytes(wl.C1) == 16_793_600
+    assert wl.kv_bytes(wl.C2) == 16_809_984
+    assert wl.kv_bytes(wl.C3_FULL) == 67_141_632
+    assert wl.kv_bytes(wl.C3_SWA) == 294_912
+    assert wl.attn_flops(wl.C4_FULL) == 137_472_507_904
+    assert wl.attn_flops(wl.C4_SWA) == 8_456_765_440
+    lens = wl.seq_lengths(wl.C5)
+    assert len(lens) == 32 and all(512 <= n <= 16384 for n in lens)
+    assert wl.kv_bytes(wl.C5) == sum(lens) * 2048 + 2 * 2_097_152
+
+
+def test_shape_mirror():
+    sh = attn.Shape(hd=128, n_kv=4, hpk=8)
+    assert sh.row() == 512 and sh.n_head == 32
+
+
+def test_small_inputs_are_deterministic():
+    a = wl.make_inputs(wl.C3_FULL.scaled(kv_len=256))
+    b = wl.make_inputs(wl.C3_FULL.scaled(kv_len=256))
+    assert (a.q == b.q).all() and (a.k == b.k).all() and (a.sinks == b.sinks).all()
