@@ -13,6 +13,7 @@ from .attn import (  # noqa: F401
     decode,
     library_path,
     load_library,
+    new_workspace,
     partials_merge,
     prefill,
     workspace_bytes,
@@ -25,6 +26,7 @@ __all__ = [
     "decode",
     "library_path",
     "load_library",
+    "new_workspace",
     "partials_merge",
     "prefill",
     "workspace_bytes",

@@ -33,6 +33,7 @@ EXPORTS = (
     "pelica_attn_version",
     "pelica_attn_last_error",
     "pelica_attn_workspace_bytes",
+    "pelica_attn_workspace_init",
     "pelica_attn_decode",
     "pelica_attn_prefill",
     "pelica_attn_partials_merge",
@@ -113,6 +114,8 @@ def load_library() -> ctypes.CDLL:
     lib.pelica_attn_last_error.argtypes = []
     lib.pelica_attn_workspace_bytes.restype = sz
     lib.pelica_attn_workspace_bytes.argtypes = [dp]
+    lib.pelica_attn_workspace_init.restype = ctypes.c_int
+    lib.pelica_attn_workspace_init.argtypes = [vp, sz, vp]
     lib.pelica_attn_decode.restype = ctypes.c_int
     lib.pelica_attn_decode.argtypes = [dp, vp, vp, vp, vp, vp, vp, sz, vp]
     lib.pelica_attn_prefill.restype = ctypes.c_int
@@ -174,6 +177,13 @@ def workspace_bytes(desc: AttnDesc) -> int:
     return n
 
 
+def new_workspace(desc: AttnDesc, device="cuda"):
+    """A zero-filled workspace for decode calls with this descriptor."""
+    import torch
+
+    return torch.zeros(max(workspace_bytes(desc), 16), dtype=torch.uint8, device=device)
+
+
 def decode(q, k, v, *, n_kv: int, kv_len: int, sinks=None, window: int = 0, ring_cap: int = 0,
            scale: Optional[float] = None, seq_kv_len=None, seq_kv_offset=None, kv_row_stride: int = 0,
            out=None, workspace=None, stream=None):
@@ -197,7 +207,8 @@ def decode(q, k, v, *, n_kv: int, kv_len: int, sinks=None, window: int = 0, ring
     if out is None:
         out = torch.empty_like(q)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
-        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+        # zero-filled once: the in-kernel combine's counters start at 0
+        workspace = torch.zeros(need, dtype=torch.uint8, device=q.device)
     if sinks is not None:
         assert sinks.dtype == torch.float32 and sinks.is_cuda and sinks.numel() == n_head
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()

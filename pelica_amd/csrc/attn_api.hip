@@ -60,6 +60,14 @@ int check_desc(const PelicaAttnDesc* d) {
                         d->kv_len - lo0);
     }
     if (!(d->scale >= 0.f) || std::isinf(d->scale)) return fail(PELICA_ATTN_EINVAL, "scale must be finite, >= 0");
+    {
+        // one sequence's rows of one kv head are addressed with 32-bit byte offsets
+        const long long stride = d->kv_row_stride ? d->kv_row_stride : (long long)d->n_kv * d->hd;
+        const long long rows = (d->ring_cap ? d->ring_cap : d->kv_len) + 128LL;
+        if (rows * stride * 2 >= (1LL << 32))
+            return fail(PELICA_ATTN_EUNSUPPORTED, "a sequence's cache span (%lld rows x %lld values) exceeds 4 GiB",
+                        rows - 128, stride);
+    }
     return PELICA_ATTN_OK;
 }
 
@@ -67,7 +75,7 @@ float eff_scale(const PelicaAttnDesc* d) { return d->scale > 0.f ? d->scale : 1.
 
 struct DecodePlan {
     int R, rt, n_rg, split_keys, n_slot;
-    size_t ws_bytes;
+    size_t ctr_bytes, ml_bytes, ws_bytes;
 };
 
 int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
@@ -82,12 +90,16 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
     // keys any row of a sequence can see
     const long long span = d->window > 0 ? std::min<long long>(d->kv_len, (long long)d->window + d->q_tokens - 1)
                                          : d->kv_len;
-    const long long blocks = ceil_div(span, 64);
-    const long long rows_of_work = (long long)d->n_seq * d->n_kv * n_rg;
-    const int target = env_int("PELICA_ATTN_DECODE_WGS", 1024);
-    int sb = env_int("PELICA_ATTN_SPLIT_BLOCKS", 0);
-    if (sb <= 0) sb = std::max<long long>(1, (blocks * rows_of_work + target - 1) / std::max(1, target));
-    int split_keys = 64 * sb, n_slot = 0;
+    const long long groups = (long long)d->n_seq * d->n_kv * n_rg;
+    const long long blocks = (long long)ceil_div(span, 64) * groups;
+    // 64-key blocks per wave: enough waves to keep ~8 per CU streaming
+    // one round of resident waves: 256 CUs x 4 SIMDs x the kernel's waves per SIMD
+    const int occ = (d->hd == 64 && rt <= 2) ? 2 : 1;
+    const int target_waves = std::max(64, env_int("PELICA_ATTN_DECODE_WAVES", 1024 * occ));
+    int spw = env_int("PELICA_ATTN_SPLIT_BLOCKS", 0);
+    if (spw <= 0) spw = (int)std::max<long long>(1, (blocks + target_waves - 1) / target_waves);
+    long long split_keys = 64LL * pelica::kDecodeWaves * spw;
+    int n_slot = 0;
     for (;;) {
         const int total = ceil_div(d->kv_len, split_keys);
         n_slot = d->window > 0 ? std::min<int>(total, ceil_div(span, split_keys) + 1) : total;
@@ -97,11 +109,13 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
     pl->R = R;
     pl->rt = rt;
     pl->n_rg = n_rg;
-    pl->split_keys = split_keys;
+    pl->split_keys = (int)split_keys;
     pl->n_slot = n_slot;
-    // (max, sum) pairs, then O rows 16-byte aligned
+    // workspace: arrival counters, (max, sum) pairs, O rows; 256-byte aligned parts
     const size_t n_part = (size_t)d->n_seq * d->n_kv * R * n_slot;
-    pl->ws_bytes = n_slot > 1 ? (((2 * n_part + 3) & ~(size_t)3) + n_part * d->hd) * sizeof(float) : 0;
+    pl->ctr_bytes = ((size_t)groups * 4 + 255) & ~(size_t)255;
+    pl->ml_bytes = (n_part * 2 * 4 + 255) & ~(size_t)255;
+    pl->ws_bytes = n_slot > 1 ? pl->ctr_bytes + pl->ml_bytes + n_part * d->hd * 4 : 0;
     return PELICA_ATTN_OK;
 }
 
@@ -146,6 +160,16 @@ size_t pelica_attn_workspace_bytes(const PelicaAttnDesc* desc) {
     return pl.ws_bytes;
 }
 
+int pelica_attn_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
+    g_err[0] = 0;
+    if (!workspace || workspace_bytes == 0) return PELICA_ATTN_OK;
+    if (misaligned(workspace)) return fail(PELICA_ATTN_EINVAL, "workspace must be 16-byte aligned");
+    hipError_t e = pelica::launch_zero(static_cast<unsigned*>(workspace), workspace_bytes / 4,
+                                       static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(PELICA_ATTN_EHIP, "workspace init: %s", hipGetErrorString(e));
+    return PELICA_ATTN_OK;
+}
+
 int pelica_attn_decode(const PelicaAttnDesc* desc, const float* q, const uint16_t* k, const uint16_t* v,
                        const float* sinks, float* out, void* workspace, size_t workspace_bytes, void* stream) {
     g_err[0] = 0;
@@ -164,9 +188,10 @@ int pelica_attn_decode(const PelicaAttnDesc* desc, const float* q, const uint16_
     p.v = v;
     p.sinks = sinks;
     p.out = out;
-    const size_t n_part = (size_t)desc->n_seq * desc->n_kv * pl.R * pl.n_slot;
-    p.ws_ml = pl.ws_bytes ? static_cast<float*>(workspace) : nullptr;
-    p.ws_o = pl.ws_bytes ? static_cast<float*>(workspace) + ((2 * n_part + 3) & ~(size_t)3) : nullptr;
+    char* ws = static_cast<char*>(workspace);
+    p.ws_ctr = pl.ws_bytes ? reinterpret_cast<unsigned*>(ws) : nullptr;
+    p.ws_ml = pl.ws_bytes ? reinterpret_cast<float*>(ws + pl.ctr_bytes) : nullptr;
+    p.ws_o = pl.ws_bytes ? reinterpret_cast<float*>(ws + pl.ctr_bytes + pl.ml_bytes) : nullptr;
     p.seq_len = desc->seq_kv_len;
     p.seq_off = desc->seq_kv_offset;
     p.row_stride = desc->kv_row_stride ? desc->kv_row_stride : (int64_t)desc->n_kv * desc->hd;
@@ -177,13 +202,14 @@ int pelica_attn_decode(const PelicaAttnDesc* desc, const float* q, const uint16_
     p.hpk = desc->n_head / desc->n_kv;
     p.T = desc->q_tokens;
     p.R = pl.R;
+    p.n_rg = pl.n_rg;
     p.n_seq = desc->n_seq;
     p.window = desc->window;
     p.ring_cap = desc->ring_cap;
     p.qscale = eff_scale(desc) * pelica::kLog2e;
     p.n_slot = pl.n_slot;
     p.split_keys = pl.split_keys;
-    hipError_t e = pelica::launch_decode(p, pl.rt, pl.n_rg, static_cast<hipStream_t>(stream));
+    hipError_t e = pelica::launch_decode(p, pl.rt, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(PELICA_ATTN_EHIP, "decode launch: %s", hipGetErrorString(e));
     return PELICA_ATTN_OK;
 }

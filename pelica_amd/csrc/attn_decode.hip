@@ -1,87 +1,235 @@
 // Split-K flash-decode for gfx950: f32 queries, f16 KV cache, f32 output.
 //
-// Work split.  A workgroup is one wave (64 lanes) and owns (sequence s, kv
-// head g, row group, key split).  All query rows that share kv head g — the
-// GQA group times the pass's tokens (drafts) — ride in the same wave, so
-// every K/V byte is read from HBM once.  Rows sit in the MFMA's 16-wide n
-// dimension; keys stream through in blocks of 64.
+// Work split.  A workgroup of NW waves owns (sequence s, kv head g, row group,
+// key split).  All query rows that share kv head g — the GQA group times the
+// pass's tokens (drafts) — ride in the same wave, so every K/V byte is read
+// from HBM once.  Rows sit in the MFMA's 16-wide n dimension; keys stream
+// through in blocks of 64, the waves of a workgroup taking every NW-th block.
 //
-// Per 64-key block:
-//   K  global -> registers with 128-bit loads, already in the A-operand
-//      layout of v_mfma_f32_16x16x32_f16 (lane: key l%16, 8 dims), so K
-//      never touches LDS;
+// Per 64-key block (software-pipelined one block ahead):
+//   K  global -> registers with 128-bit loads, directly in the A-operand
+//      layout of v_mfma_f32_16x16x32_f16 (lane: key l%16, 8 dims): K never
+//      touches LDS; the next block's K is in flight while this one computes;
 //   S^T[key][row] = K Q^T on MFMA.  Q is split into f16 hi + lo parts (two
 //      MFMAs) so the scores keep ~fp32 accuracy;
-//   online softmax in base 2 (log2(e) folded into the query scale), block
+//   online softmax in base 2 (log2(e) folded into the query scale); block
 //      max and sums over the four 16-lane groups with permlane swaps;
-//   V  global -> registers -> LDS (128-bit, row-major), read back with the
-//      transposing ds_read_b64_tr_b16 into the A operand of O^T = V^T P^T;
-//      P (f32) is split into f16 hi + lo as the B operand, straight from the
-//      score registers (its key order matches the A operand's).
-// Each split writes (max, sum, O[hd]) per row to the workspace; a combine
-// kernel merges the splits in key order with the head's sink.  A single
-// split writes the normalised output itself.
+//   V  global -> registers (prefetched with K) -> the wave's LDS buffer
+//      (128-bit stores, XOR-swizzled 16-byte pieces), read back with the
+//      transposing ds_read_b64_tr_b16 as the A operand of O^T = V^T P^T; P is
+//      split into f16 hi + lo as the B operand, straight from the score
+//      registers (its key order matches the A operand's).
+// The NW wave states merge through LDS into one partial (max, sum, O) per row
+// and split.  The last workgroup of a (sequence, kv head, row group) to
+// finish — an agent-scope atomic counter in the workspace — combines the
+// splits in key order with the head's sink and writes the output, so a
+// decode call is one kernel launch.  A single split writes the output
+// directly.
 //
 // Reference semantics: src/moe_kernels.rs:482-617 (attn_dec, merge_dec),
 // src/oss_batch.rs:172-251 (ATTN_T: window, ring, sink), :253-425 (attn_s +
 // ATTN_M: split partials, sink in max and denominator).
+#include <algorithm>
+
 #include "attn_decode.hpp"
 
 namespace pelica {
 
-template <int HD, int RT>
-__global__ __launch_bounds__(64) void decode_split_kernel(DecodeParams p) {
-    constexpr int DS = HD / 32;  // 32-dim k-steps of the QK^T MFMA
-    constexpr int DT = HD / 16;  // 16-dim output tiles
-    constexpr int VP = HD + 8;   // LDS row pitch in halfs (breaks bank aliasing)
-    constexpr int VPL = HD / 8;  // 16-byte V pieces per lane per block
-    __shared__ __attribute__((aligned(16))) _Float16 vl[64 * VP];
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, 64));
+    return x;
+}
 
-    const int lane = threadIdx.x, g = lane >> 4, c16 = lane & 15;
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
+    return x;
+}
+
+// Partials cross workgroups (and XCDs, whose L2s are not coherent with each
+// other) through agent-scope atomic accesses: these write through to / read
+// from the device-coherent level, so no L2 writeback or invalidate of the
+// whole cache is needed around the arrival counter.
+__device__ __forceinline__ void store_coherent(float* p, float a, float b) {
+    const uint64_t v = (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(b) << 32);
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float2 load_coherent(const float* p) {
+    const uint64_t v =
+        __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
+}
+
+// waves per SIMD the decode kernel is compiled for (register budget 512/n)
+template <int HD, int RT>
+#ifndef PELICA_OCC64
+#define PELICA_OCC64 3
+#endif
+#ifndef PELICA_DEPTH64
+#define PELICA_DEPTH64 1
+#endif
+constexpr int kDecodeOcc = HD == 64 ? (RT == 1 ? PELICA_OCC64 : RT == 2 ? 2 : 1) : 1;
+
+// f16 parts the decode kernel splits Q and P into: 2 (hi + lo, ~fp32
+// products) or 1 (f16 only)
+#ifndef PELICA_DECODE_PARTS
+#define PELICA_DECODE_PARTS 2
+#endif
+constexpr int kDecodeSplitParts = PELICA_DECODE_PARTS;
+
+// blocks in flight per wave (register budget)
+template <int HD, int RT>
+constexpr int kDecodeDepth = (HD == 64 && RT == 1) ? PELICA_DEPTH64 : 1;
+
+// word 3 of a gfx9 buffer resource: 32-bit data format, raw addressing
+constexpr int kBufferFlags = 0x00020000;
+
+// Visible keys of one query: [lo, pos].
+struct KeyRange {
+    int lo, pos;
+};
+
+__device__ __forceinline__ KeyRange key_range(int len, int T, int t, int window) {
+    const int pos = len - T + t;
+    return KeyRange{(window > 0 && pos + 1 > window) ? pos + 1 - window : 0, pos};
+}
+
+// LDS byte offset of 16-byte piece p of key row k in a V block: rows of HD
+// halfs, pieces XOR-swizzled so the transposed reads of 4 consecutive keys
+// hit distinct banks.
+template <int HD>
+__device__ __forceinline__ int v_slot(int k, int p) {
+    return k * (HD * 2) + ((p ^ ((k & 3) << 1)) << 4);
+}
+
+template <int HD>
+__device__ __forceinline__ const _Float16* v_elem(const _Float16* base, int k, int d) {
+    return reinterpret_cast<const _Float16*>(reinterpret_cast<const char*>(base) + v_slot<HD>(k, d >> 3) +
+                                             ((d & 7) << 1));
+}
+
+template <int HD, int RT, int NW, bool RING, int D>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecodeOcc<HD, RT>, 8))) void decode_kernel(DecodeParams p) {
+    constexpr int DS = HD / 32;   // 32-dim k-steps of the QK^T MFMA
+    constexpr int DT = HD / 16;   // 16-dim output tiles
+    constexpr int VPL = HD / 8;   // 16-byte V pieces per lane per block
+    constexpr int ROWS = RT * 16;
+    constexpr int NP = kDecodeSplitParts;              // f16 parts of Q and P (hi, lo)
+    constexpr int VBUF = 64 * HD * 2;                  // bytes of one wave's V block
+    constexpr int MERGE = NW * ROWS * (HD + 2) * 4;    // bytes of the wave-merge area
+    // bytes of the split combine: weights, 1/sum, per-phase partial sums
+    constexpr int WTS = (ROWS * kMaxSlots + ROWS) * 4 + 64 * NW * 16;
+    constexpr int SMEM1 = VBUF * NW > MERGE ? VBUF * NW : MERGE;
+    constexpr int SMEM = SMEM1 > WTS ? SMEM1 : WTS;
+    __shared__ __attribute__((aligned(16))) char smem[SMEM];
+    __shared__ int s_last;
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
     const int kvh = blockIdx.y % p.n_kv, rg = blockIdx.y / p.n_kv;
     const int s = blockIdx.z;
     const int len = p.seq_len ? p.seq_len[s] : p.kv_len;
     if (len < p.T || len <= 0) return;
     const int64_t row0 = p.seq_off ? p.seq_off[s] : (int64_t)s * (p.ring_cap ? p.ring_cap : p.kv_len);
-    const int pos_first = len - p.T;
-    const int lo_min = (p.window > 0 && pos_first + 1 > p.window) ? pos_first + 1 - p.window : 0;
+    const int lo_min = key_range(len, p.T, 0, p.window).lo;
     const int split0 = lo_min / p.split_keys;
+    const int n_active = min(p.n_slot, (len - 1) / p.split_keys - split0 + 1);
     const int slot = blockIdx.x;
+    if (slot >= n_active) return;
     const int kbeg = (split0 + slot) * p.split_keys;
     const int kend = min(kbeg + p.split_keys, len);
-    if (kbeg >= kend) return;
+    const int rbase = rg * ROWS;
 
-    // queries of this lane's rows: hi/lo f16 pairs, scaled into base 2
-    half8 qh[RT][DS], ql[RT][DS];
+    // ---- K/V stream setup: the first D blocks are requested before
+    //      anything else, so their HBM latency overlaps the query setup ----
+    // Buffer resources over this sequence's rows of kv head kvh: 32-bit
+    // offsets, and loads at offsets past num_records return 0 without
+    // touching memory — the tail of the last block, and the prefetches
+    // that run past a wave's last block, cost no traffic.
+    const uint32_t stride_b = (uint32_t)p.row_stride * 2;
+    const uint32_t nrec = (RING ? (uint32_t)p.ring_cap : (uint32_t)len) * stride_b;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.k + row0 * p.row_stride + (size_t)kvh * HD), (short)0, (int)nrec, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.v + row0 * p.row_stride + (size_t)kvh * HD), (short)0, (int)nrec, kBufferFlags);
+    // V piece slot i*64+lane of a block holds key i*KPL + lane/PPR and the
+    // swizzled 16-byte piece of lane%PPR; the key's low two bits (the
+    // swizzle) depend on the lane only, so one lane offset serves every i
+    constexpr int PPR = HD / 8;         // 16-byte pieces per key row
+    constexpr int KPL = 64 / PPR;       // keys per 64 lanes
+    const int vk0 = lane / PPR;
+    const uint32_t vcol = 16 * ((lane % PPR) ^ ((vk0 & 3) << 1));
+    // this wave's blocks: kb = kfirst + 64 * (wave + NW * i)
+    int kfirst = kbeg;
+    if (lo_min > kbeg) kfirst = kbeg + ((lo_min - kbeg) & ~63);
+    const int nblk_all = (kend - kfirst + 63) / 64;
+    const int nb = nblk_all > wave ? (nblk_all - wave + NW - 1) / NW : 0;
+    char* vlds = smem + wave * VBUF;
+    auto blk = [&](int i) { return kfirst + 64 * (wave + NW * i); };
+
+    // D blocks in flight: K straight into MFMA-operand registers, V into
+    // staging registers
+    half8 kr[D][4][DS];
+    u32x4 vr[D][VPL];
+    auto issue = [&](half8 (&kd)[4][DS], u32x4 (&vd)[VPL], int i) {
+        const bool valid = i < nb;
+        const int kb = blk(i);
+        if (!RING) {
+            const uint32_t base = valid ? (uint32_t)kb * stride_b : nrec;
+#pragma unroll
+            for (int j = 0; j < VPL; ++j)
+                vd[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      rv, base + (KPL * j + vk0) * stride_b + vcol, 0, 0));
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                for (int ds = 0; ds < DS; ++ds)
+                    kd[kt][ds] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(
+                                                               rk, base + (16 * kt + c16) * stride_b + 16 * g + 64 * ds,
+                                                               0, 0));
+        } else {
+#pragma unroll
+            for (int j = 0; j < VPL; ++j) {
+                const uint32_t off = valid ? ((kb + KPL * j + vk0) % p.ring_cap) * stride_b + vcol : nrec;
+                vd[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
+            }
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) {
+                const uint32_t off = valid ? ((kb + 16 * kt + c16) % p.ring_cap) * stride_b + 16 * g : nrec;
+#pragma unroll
+                for (int ds = 0; ds < DS; ++ds)
+                    kd[kt][ds] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rk, off + 64 * ds, 0, 0));
+            }
+        }
+    };
+#pragma unroll
+    for (int sl = 0; sl < D; ++sl) issue(kr[sl], vr[sl], sl);
+
+    // ---- queries of this lane's rows: f16 parts (hi[, lo]) in base 2 ----
+    half8 qf[NP][RT][DS];
     int posr[RT], lor[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-        const int r = rg * 16 * RT + 16 * rt + c16;
-        if (r < p.R) {
-            const int t = r / p.hpk, h = kvh * p.hpk + r % p.hpk;
-            const float* qp = p.q + ((size_t)(s * p.T + t) * p.n_head + h) * HD + 8 * g;
-            posr[rt] = pos_first + t;
-            lor[rt] = (p.window > 0 && posr[rt] + 1 > p.window) ? posr[rt] + 1 - p.window : 0;
+        const int r = rbase + 16 * rt + c16;
+        const bool rv_ok = r < p.R;
+        const int rr = rv_ok ? r : 0;
+        const int t = rr / p.hpk, h = kvh * p.hpk + rr % p.hpk;
+        const float* qp = p.q + ((size_t)(s * p.T + t) * p.n_head + h) * HD + 8 * g;
+        const KeyRange krg = key_range(len, p.T, t, p.window);
+        posr[rt] = rv_ok ? krg.pos : -1;
+        lor[rt] = krg.lo;
 #pragma unroll
-            for (int ds = 0; ds < DS; ++ds) {
-                const float4v a = *reinterpret_cast<const float4v*>(qp + 32 * ds);
-                const float4v b = *reinterpret_cast<const float4v*>(qp + 32 * ds + 4);
+        for (int ds = 0; ds < DS; ++ds) {
+            const float4v a = *reinterpret_cast<const float4v*>(qp + 32 * ds);
+            const float4v b = *reinterpret_cast<const float4v*>(qp + 32 * ds + 4);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    _Float16 hi, lo;
-                    split_f16(a[j] * p.qscale, hi, lo);
-                    qh[rt][ds][j] = hi; ql[rt][ds][j] = lo;
-                    split_f16(b[j] * p.qscale, hi, lo);
-                    qh[rt][ds][4 + j] = hi; ql[rt][ds][4 + j] = lo;
-                }
+            for (int j = 0; j < 8; ++j) {
+                const float x = rv_ok ? (j < 4 ? a[j] : b[j - 4]) * p.qscale : 0.f;
+                const _Float16 hi = (_Float16)x;
+                qf[0][rt][ds][j] = hi;
+                if (NP > 1) qf[NP - 1][rt][ds][j] = (_Float16)(x - (float)hi);
             }
-        } else {
-            posr[rt] = -1;
-            lor[rt] = 0;
-#pragma unroll
-            for (int ds = 0; ds < DS; ++ds)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) { qh[rt][ds][j] = 0; ql[rt][ds][j] = 0; }
         }
     }
 
@@ -95,55 +243,38 @@ __global__ __launch_bounds__(64) void decode_split_kernel(DecodeParams p) {
         for (int dt = 0; dt < DT; ++dt) o[dt][rt] = float4v{0.f, 0.f, 0.f, 0.f};
     }
 
-    const uint16_t* kbase = p.k + (size_t)kvh * HD;
-    const uint16_t* vbase = p.v + (size_t)kvh * HD;
-    auto row_of = [&](int key) -> int64_t {
-        key = min(key, kend - 1);
-        return row0 + (p.ring_cap ? key % p.ring_cap : key);
+    auto stage_v = [&](const u32x4 (&vs)[VPL]) {
+        // previous block's transposed reads are done (in-order LDS, same wave)
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) *reinterpret_cast<u32x4*>(vlds + (j * 64 + lane) * 16) = vs[j];
+        __builtin_amdgcn_wave_barrier();
     };
-
-    int kb = kbeg;
-    if (lo_min > kbeg) kb = kbeg + ((lo_min - kbeg) & ~63);
-    for (; kb < kend; kb += 64) {
-        half8 kr[4][DS];
+    float4v sc[4][RT];
+    auto qk = [&](const half8 (&kc)[4][DS]) {
+        // independent accumulators per (part, key tile, row tile); the
+        // k-steps run outermost so consecutive MFMAs do not depend on each other
+        float4v acc[NP][4][RT];
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-            const uint16_t* kp = kbase + row_of(kb + 16 * kt + c16) * p.row_stride + 8 * g;
+        for (int pp = 0; pp < NP; ++pp)
 #pragma unroll
-            for (int ds = 0; ds < DS; ++ds) kr[kt][ds] = load16(kp + 32 * ds);
-        }
-        u32x4 vr[VPL];
+            for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-            const int piece = i * 64 + lane;
-            const int key = piece / (HD / 8), col = piece % (HD / 8);
-            vr[i] = *reinterpret_cast<const u32x4*>(vbase + row_of(kb + key) * p.row_stride + 8 * col);
-        }
-
-        // S^T = K Q^T (4 key tiles x RT row tiles), hi + lo queries
-        float4v sc[4][RT];
+                for (int rt = 0; rt < RT; ++rt) acc[pp][kt][rt] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+            for (int pp = 0; pp < NP; ++pp)
+#pragma unroll
+                for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt) acc[pp][kt][rt] = mfma16(kc[kt][ds], qf[pp][rt][ds], acc[pp][kt][rt]);
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt) {
-                float4v acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int ds = 0; ds < DS; ++ds) {
-                    acc = mfma16(kr[kt][ds], qh[rt][ds], acc);
-                    acc = mfma16(kr[kt][ds], ql[rt][ds], acc);
-                }
-                sc[kt][rt] = acc;
-            }
-
-        // V block into LDS (the previous block's reads are complete)
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-            const int piece = i * 64 + lane;
-            const int key = piece / (HD / 8), col = piece % (HD / 8);
-            *reinterpret_cast<u32x4*>(&vl[key * VP + 8 * col]) = vr[i];
-        }
-
+            for (int rt = 0; rt < RT; ++rt) sc[kt][rt] = NP > 1 ? acc[0][kt][rt] + acc[NP - 1][kt][rt] : acc[0][kt][rt];
+    };
+    auto softmax_pv = [&](int kb) {
         // mask: row r sees keys [lor, posr]
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
@@ -154,9 +285,7 @@ __global__ __launch_bounds__(64) void decode_split_kernel(DecodeParams p) {
                 for (int rt = 0; rt < RT; ++rt)
                     if (key < lor[rt] || key > posr[rt]) sc[kt][rt][i] = -INFINITY;
             }
-
-        // online softmax, base 2
-        half8 ph[RT][2], pl[RT][2];
+        half8 pf[NP][RT][2];
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
             float bm = -INFINITY;
@@ -176,141 +305,232 @@ __global__ __launch_bounds__(64) void decode_split_kernel(DecodeParams p) {
                 for (int i = 0; i < 4; ++i) {
                     const float pe = fast_exp2(sc[kt][rt][i] - ms);
                     ls += pe;
-                    _Float16 hi, lo;
-                    split_f16(pe, hi, lo);
-                    ph[rt][kt >> 1][(kt & 1) * 4 + i] = hi;
-                    pl[rt][kt >> 1][(kt & 1) * 4 + i] = lo;
+                    const _Float16 hi = (_Float16)pe;
+                    pf[0][rt][kt >> 1][(kt & 1) * 4 + i] = hi;
+                    if (NP > 1) pf[NP - 1][rt][kt >> 1][(kt & 1) * 4 + i] = (_Float16)(pe - (float)hi);
                 }
             l[rt] = l[rt] * c + ls;
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) o[dt][rt] *= c;
         }
+        // O^T += V^T P^T; the dim tiles are independent accumulators
+        const _Float16* vb = reinterpret_cast<const _Float16*>(vlds);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            half8 va[DT];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const int k0 = 32 * u + 4 * g + (c16 >> 2), d0 = 16 * dt + 4 * (c16 & 3);
+                va[dt] = cat8(lds_read_tr(v_elem<HD>(vb, k0, d0)), lds_read_tr(v_elem<HD>(vb, k0 + 16, d0)));
+            }
+#pragma unroll
+            for (int pp = 0; pp < NP; ++pp)
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt) o[dt][rt] = mfma16(va[dt], pf[pp][rt][u], o[dt][rt]);
+        }
+    };
 
-        __syncthreads();
-        // O^T += V^T P^T
+    // Pipeline D blocks deep.  Every trip issues the block D ahead (beyond
+    // the wave's range such loads are out of bounds and free), so the wait
+    // counts are the same on every trip.
+    for (int i = 0; i < nb; i += D) {
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const _Float16* a = vl + (32 * u + 4 * g + (c16 >> 2)) * VP + 16 * dt + 4 * (c16 & 3);
-                const half8 va = cat8(lds_read_tr(a), lds_read_tr(a + 16 * VP));
-#pragma unroll
-                for (int rt = 0; rt < RT; ++rt) {
-                    o[dt][rt] = mfma16(va, ph[rt][u], o[dt][rt]);
-                    o[dt][rt] = mfma16(va, pl[rt][u], o[dt][rt]);
-                }
+        for (int sl = 0; sl < D; ++sl) {
+            if (i + sl < nb) {
+                stage_v(vr[sl]);
+                qk(kr[sl]);
+                issue(kr[sl], vr[sl], i + sl + D);
+                softmax_pv(blk(i + sl));
             }
-    }
-
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-        const float lt = group4_sum(l[rt]);
-        const int r = rg * 16 * RT + 16 * rt + c16;
-        if (r >= p.R) continue;
-        if (p.n_slot == 1) {
-            // one split: normalise here, sink in max and denominator
-            const int t = r / p.hpk, h = kvh * p.hpk + r % p.hpk;
-            float w = 1.f, L = lt;
-            if (p.sinks) {
-                const float sk = p.sinks[h] * kLog2e;
-                const float M = fmaxf(m[rt], sk);
-                w = fast_exp2(m[rt] - M);
-                L = lt * w + fast_exp2(sk - M);
-            }
-            const float f = w / L;
-            float* op = p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + 4 * g;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
-                *reinterpret_cast<float4v*>(op + 16 * dt) = o[dt][rt] * f;
-        } else {
-            const size_t idx = ((size_t)(s * p.n_kv + kvh) * p.R + r) * p.n_slot + slot;
-            if (g == 0) {
-                p.ws_ml[2 * idx] = m[rt];
-                p.ws_ml[2 * idx + 1] = lt;
-            }
-            float* op = p.ws_o + idx * HD + 4 * g;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<float4v*>(op + 16 * dt) = o[dt][rt];
         }
     }
-}
 
-__device__ __forceinline__ float wave_max(float x) {
+    // ---- merge the NW wave states of each row through LDS ----
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, 64));
-    return x;
-}
-
-__device__ __forceinline__ float wave_sum(float x) {
+    for (int rt = 0; rt < RT; ++rt) l[rt] = group4_sum(l[rt]);
+    __syncthreads();  // V buffers are free
+    float* mo = reinterpret_cast<float*>(smem);            // [NW][ROWS][HD] O
+    float* mml = mo + NW * ROWS * HD;                       // [NW][ROWS][2] (m, l)
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
-    return x;
-}
-
-// Combine of one row's split partials in key order, with the sink
-// (src/moe_kernels.rs:585-617 merge_dec, src/oss_batch.rs:395-425 ATTN_M).
-// Grid (n_kv * R, n_seq), 64 lanes.
-template <int HD>
-__global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
-    __shared__ float w[kMaxSlots];
-    const int lane = threadIdx.x;
-    const int kvh = blockIdx.x / p.R, r = blockIdx.x % p.R;
-    const int s = blockIdx.y;
-    const int len = p.seq_len ? p.seq_len[s] : p.kv_len;
-    if (len < p.T || len <= 0) return;
-    const int t = r / p.hpk, h = kvh * p.hpk + r % p.hpk;
-    const int pos_first = len - p.T;
-    const int lo_min = (p.window > 0 && pos_first + 1 > p.window) ? pos_first + 1 - p.window : 0;
-    const int split0 = lo_min / p.split_keys;
-    const int pos = pos_first + t;
-    const int lo = (p.window > 0 && pos + 1 > p.window) ? pos + 1 - p.window : 0;
-    const int c0 = lo / p.split_keys - split0, c1 = pos / p.split_keys - split0;
-    const size_t base = ((size_t)(s * p.n_kv + kvh) * p.R + r) * p.n_slot;
-
-    const float sk = p.sinks ? p.sinks[h] * kLog2e : -INFINITY;
-    float M = sk;
-    for (int c = c0 + lane; c <= c1; c += 64) M = fmaxf(M, p.ws_ml[2 * (base + c)]);
-    M = wave_max(M);
-    const float ms = (M == -INFINITY) ? 0.f : M;
-    float L = 0.f;
-    for (int c = c0 + lane; c <= c1; c += 64) {
-        const float wc = fast_exp2(p.ws_ml[2 * (base + c)] - ms);
-        w[c - c0] = wc;
-        L += p.ws_ml[2 * (base + c) + 1] * wc;
+    for (int rt = 0; rt < RT; ++rt) {
+        const int row = 16 * rt + c16;
+        float* dst = mo + (wave * ROWS + row) * HD + 4 * g;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<float4v*>(dst + 16 * dt) = o[dt][rt];
+        if (g == 0) {
+            mml[(wave * ROWS + row) * 2] = m[rt];
+            mml[(wave * ROWS + row) * 2 + 1] = l[rt];
+        }
     }
-    L = wave_sum(L);
-    if (p.sinks) L += fast_exp2(sk - ms);
     __syncthreads();
-    const float inv = 1.f / L;
-    float* op = p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD;
-    for (int d = lane; d < HD; d += 64) {
-        float acc = 0.f;
-        for (int c = c0; c <= c1; ++c) acc += p.ws_o[(base + c) * HD + d] * w[c - c0];
-        op[d] = acc * inv;
+
+    const int rows_here = min(ROWS, p.R - rbase);
+    const size_t grp = (size_t)(s * p.n_kv + kvh) * p.n_rg + rg;
+    // (row, 4-dim chunk) items of the workgroup's result
+    constexpr int D4 = HD / 4;
+    for (int it = tid; it < rows_here * D4; it += 64 * NW) {
+        const int row = it / D4, d = 4 * (it % D4);
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, mml[(w * ROWS + row) * 2]);
+        const float ms = (M == -INFINITY) ? 0.f : M;
+        float L = 0.f;
+        float4v O = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const float wt = fast_exp2(mml[(w * ROWS + row) * 2] - ms);
+            L += mml[(w * ROWS + row) * 2 + 1] * wt;
+            O += *reinterpret_cast<const float4v*>(mo + (w * ROWS + row) * HD + d) * wt;
+        }
+        const int r = rbase + row;
+        if (n_active == 1) {
+            // the only split: normalise here, sink in max and denominator
+            const int t = r / p.hpk, h = kvh * p.hpk + r % p.hpk;
+            float f;
+            if (p.sinks) {
+                const float sk = p.sinks[h] * kLog2e;
+                const float M2 = fmaxf(M, sk);
+                const float wgt = fast_exp2(ms - M2);
+                f = wgt / (L * wgt + fast_exp2(sk - M2));
+            } else {
+                f = 1.f / L;
+            }
+            *reinterpret_cast<float4v*>(p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + d) = O * f;
+        } else {
+            const size_t idx = ((size_t)(s * p.n_kv + kvh) * p.R + r) * p.n_slot + slot;
+            if (d == 0) store_coherent(p.ws_ml + 2 * idx, M, L);
+            store_coherent(p.ws_o + idx * HD + d, O[0], O[1]);
+            store_coherent(p.ws_o + idx * HD + d + 2, O[2], O[3]);
+        }
     }
+    if (n_active == 1) return;
+
+    // ---- last workgroup of the group combines the splits ----
+    // the coherent partial stores are complete before the arrival counts
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned old = __hip_atomic_fetch_add(p.ws_ctr + grp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = (old == (unsigned)n_active - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    float* wts = reinterpret_cast<float*>(smem);               // [ROWS][kMaxSlots] weights
+    float* inv = wts + ROWS * kMaxSlots;                        // [ROWS] 1/L
+    float4v* red = reinterpret_cast<float4v*>(inv + ROWS);     // [phases][pairs] partial sums
+    // per row (one wave each): max over its splits, weights, denominator
+    constexpr int SPL = kMaxSlots / 64;  // splits per lane
+    for (int row = wave; row < rows_here; row += NW) {
+        const int r = rbase + row;
+        const int t = r / p.hpk, h = kvh * p.hpk + r % p.hpk;
+        const KeyRange krg = key_range(len, p.T, t, p.window);
+        const int c0 = krg.lo / p.split_keys - split0, c1 = krg.pos / p.split_keys - split0;
+        const size_t base = ((size_t)(s * p.n_kv + kvh) * p.R + r) * p.n_slot;
+        const float sk = p.sinks ? p.sinks[h] * kLog2e : -INFINITY;
+        float2 ml[SPL];
+        float M = sk;
+#pragma unroll
+        for (int j = 0; j < SPL; ++j) {
+            const int c = lane + 64 * j;
+            ml[j] = (c >= c0 && c <= c1) ? load_coherent(p.ws_ml + 2 * (base + c)) : make_float2(-INFINITY, 0.f);
+            M = fmaxf(M, ml[j].x);
+        }
+        M = wave_max(M);
+        const float ms = (M == -INFINITY) ? 0.f : M;
+        float L = 0.f;
+#pragma unroll
+        for (int j = 0; j < SPL; ++j) {
+            const int c = lane + 64 * j;
+            const float wc = fast_exp2(ml[j].x - ms);
+            L += ml[j].y * wc;
+            wts[row * kMaxSlots + c] = wc;
+        }
+        L = wave_sum(L);
+        if (p.sinks) L += fast_exp2(sk - ms);
+        if (lane == 0) inv[row] = 1.f / L;
+    }
+    __syncthreads();
+    // O: each (row, 4-dim chunk) pair is summed over the splits by `phases`
+    // threads (split c goes to phase c % phases), then the phases in order
+    const int pairs = rows_here * D4;
+    const int phases = max(1, (64 * NW) / pairs);
+    for (int pr0 = 0; pr0 < pairs; pr0 += 64 * NW) {
+        const int pr = pr0 + tid % min(pairs - pr0, 64 * NW);
+        const int ph = pairs - pr0 >= 64 * NW ? 0 : tid / (pairs - pr0);
+        float4v acc = {0.f, 0.f, 0.f, 0.f};
+        if (ph < phases) {
+            const int row = pr / D4, d = 4 * (pr % D4);
+            const size_t base = ((size_t)(s * p.n_kv + kvh) * p.R + rbase + row) * p.n_slot;
+            const float* w = wts + row * kMaxSlots;
+            // 16 splits' loads in flight at once per pass
+            for (int c0 = ph; c0 < n_active; c0 += 16 * phases) {
+                float2 a[16], b[16];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const int c = c0 + j * phases;
+                    if (c < n_active) {
+                        a[j] = load_coherent(p.ws_o + (base + c) * HD + d);
+                        b[j] = load_coherent(p.ws_o + (base + c) * HD + d + 2);
+                    } else {
+                        a[j] = b[j] = make_float2(0.f, 0.f);
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const int c = c0 + j * phases;
+                    const float wc = c < n_active ? w[c] : 0.f;
+                    acc += float4v{a[j].x, a[j].y, b[j].x, b[j].y} * wc;
+                }
+            }
+            red[ph * min(pairs - pr0, 64 * NW) + (pr - pr0)] = acc;
+        }
+        __syncthreads();
+        if (tid < min(pairs - pr0, 64 * NW)) {
+            const int prr = pr0 + tid;
+            const int row = prr / D4, d = 4 * (prr % D4);
+            const int r = rbase + row;
+            const int t = r / p.hpk, h = kvh * p.hpk + r % p.hpk;
+            float4v sum = red[tid];
+            for (int q = 1; q < phases; ++q) sum += red[q * min(pairs - pr0, 64 * NW) + tid];
+            *reinterpret_cast<float4v*>(p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + d) = sum * inv[row];
+        }
+        __syncthreads();
+    }
+    if (tid == 0) __hip_atomic_store(p.ws_ctr + grp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int HD, int RT>
-static hipError_t launch_split(const DecodeParams& p, dim3 grid, hipStream_t st) {
-    hipLaunchKernelGGL((decode_split_kernel<HD, RT>), grid, dim3(64), 0, st, p);
+template <int HD, int RT, int NW>
+static hipError_t launch_k(const DecodeParams& p, hipStream_t st) {
+    dim3 grid(p.n_slot, p.n_kv * p.n_rg, p.n_seq);
+    constexpr int D = kDecodeDepth<HD, RT>;
+    if (p.ring_cap) hipLaunchKernelGGL((decode_kernel<HD, RT, NW, true, D>), grid, dim3(64 * NW), 0, st, p);
+    else hipLaunchKernelGGL((decode_kernel<HD, RT, NW, false, D>), grid, dim3(64 * NW), 0, st, p);
     return hipGetLastError();
 }
 
-hipError_t launch_decode(const DecodeParams& p, int rt, int n_rg, hipStream_t st) {
-    dim3 grid(p.n_slot, p.n_kv * n_rg, p.n_seq);
-    hipError_t e = hipErrorInvalidValue;
+hipError_t launch_decode(const DecodeParams& p, int rt, hipStream_t st) {
     if (p.hd == 64) {
-        if (rt == 1) e = launch_split<64, 1>(p, grid, st);
-        else if (rt == 2) e = launch_split<64, 2>(p, grid, st);
-        else if (rt == 4) e = launch_split<64, 4>(p, grid, st);
+        if (rt == 1) return launch_k<64, 1, kDecodeWaves>(p, st);
+        if (rt == 2) return launch_k<64, 2, kDecodeWaves>(p, st);
+        if (rt == 4) return launch_k<64, 4, kDecodeWaves>(p, st);
     } else if (p.hd == 128) {
-        if (rt == 1) e = launch_split<128, 1>(p, grid, st);
-        else if (rt == 2) e = launch_split<128, 2>(p, grid, st);
+        if (rt == 1) return launch_k<128, 1, kDecodeWaves>(p, st);
+        if (rt == 2) return launch_k<128, 2, kDecodeWaves>(p, st);
     }
-    if (e != hipSuccess || p.n_slot == 1) return e;
-    dim3 cgrid(p.n_kv * p.R, p.n_seq);
-    if (p.hd == 64) hipLaunchKernelGGL((decode_combine_kernel<64>), cgrid, dim3(64), 0, st, p);
-    else hipLaunchKernelGGL((decode_combine_kernel<128>), cgrid, dim3(64), 0, st, p);
+    return hipErrorInvalidValue;
+}
+
+// fill kernel for the workspace counters (graph-capturable, no memset node)
+__global__ void zero_u32_kernel(unsigned* p, size_t n) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0;
+}
+
+hipError_t launch_zero(unsigned* p, size_t n, hipStream_t st) {
+    if (!n) return hipSuccess;
+    const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 1024);
+    hipLaunchKernelGGL(zero_u32_kernel, dim3(blocks), dim3(256), 0, st, p, n);
     return hipGetLastError();
 }
 

@@ -1,11 +1,14 @@
-// Launch parameters of the decode kernels (attn_decode.hip).
+// Launch parameters of the decode kernel (attn_decode.hip).
 #pragma once
 #include "attn_common.hpp"
 
 namespace pelica {
 
-// most key splits one row can have (combine stages one weight per split in LDS)
-constexpr int kMaxSlots = 4096;
+// most key splits one (sequence, kv head, row group) may have: the last
+// workgroup stages one weight per split and row in LDS
+constexpr int kMaxSlots = 256;
+// waves per decode workgroup
+constexpr int kDecodeWaves = 4;
 
 struct DecodeParams {
     const float* q;
@@ -13,18 +16,21 @@ struct DecodeParams {
     const uint16_t* v;
     const float* sinks;
     float* out;
-    float* ws_ml;  // [n_seq][n_kv][R][n_slot] x (max, sum), base-2 max
-    float* ws_o;   // [n_seq][n_kv][R][n_slot][hd]
+    unsigned* ws_ctr;  // [n_seq][n_kv][n_rg] arrival counters, zero between calls
+    float* ws_ml;      // [n_seq][n_kv][R][n_slot] x (max, sum), base-2 max
+    float* ws_o;       // [n_seq][n_kv][R][n_slot][hd]
     const int32_t* seq_len;
     const int64_t* seq_off;
     int64_t row_stride;  // f16 values between cache rows
-    int kv_len, n_head, n_kv, hd, hpk, T, R, n_seq;
+    int kv_len, n_head, n_kv, hd, hpk, T, R, n_seq, n_rg;
     int window, ring_cap;
     float qscale;        // scale * log2(e)
-    int n_slot;          // key splits per (sequence, kv head) in the grid
+    int n_slot;          // key splits per (sequence, kv head, row group) in the grid
     int split_keys;      // keys per split, a multiple of 64
 };
 
-hipError_t launch_decode(const DecodeParams& p, int rt, int n_rg, hipStream_t st);
+hipError_t launch_decode(const DecodeParams& p, int rt, hipStream_t st);
+// zero n counters with a fill kernel (graph-capturable)
+hipError_t launch_zero(unsigned* p, size_t n, hipStream_t st);
 
 }  // namespace pelica
