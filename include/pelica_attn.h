@@ -73,18 +73,17 @@ int pelica_attn_version(void);
 const char* pelica_attn_last_error(void);
 
 /* Bytes of device workspace pelica_attn_decode needs for this descriptor
- * (split-K partials and the arrival counters of their in-kernel combine).
- * 0 on an invalid descriptor (see last_error) or when the call needs none.
- * A workspace must be zero-filled once before its first use (hipMemset or
- * pelica_attn_workspace_init); every decode call leaves it ready for the
- * next.  Calls that share one workspace must be ordered on one stream.
+ * (split-K partials).  0 on an invalid descriptor (see last_error) or when
+ * the call needs none.  Its contents need no initialisation; calls that
+ * share one workspace must be ordered on one stream.
  * Replaces the partials buffer `part` (src/moe.rs:949-952) and the split
  * partials of attn_s (src/oss.rs:573-576). */
 size_t pelica_attn_workspace_bytes(const PelicaAttnDesc* desc);
 
 /* Zero-fill a workspace on `stream` with a fill kernel (safe to record in a
- * HIP graph).  No counterpart in the reference, whose wgpu buffers start
- * zeroed at creation (src/moe.rs:949-952). */
+ * HIP graph).  Decode does not require it; it exists for callers that want
+ * deterministic workspace contents.  No counterpart in the reference, whose
+ * wgpu buffers start zeroed at creation (src/moe.rs:949-952). */
 int pelica_attn_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
 
 /* Decode attention: f32 queries over the f16 cache, f32 output, split-K

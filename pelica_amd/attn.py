@@ -178,10 +178,10 @@ def workspace_bytes(desc: AttnDesc) -> int:
 
 
 def new_workspace(desc: AttnDesc, device="cuda"):
-    """A zero-filled workspace for decode calls with this descriptor."""
+    """A workspace for decode calls with this descriptor."""
     import torch
 
-    return torch.zeros(max(workspace_bytes(desc), 16), dtype=torch.uint8, device=device)
+    return torch.empty(max(workspace_bytes(desc), 16), dtype=torch.uint8, device=device)
 
 
 def decode(q, k, v, *, n_kv: int, kv_len: int, sinks=None, window: int = 0, ring_cap: int = 0,
@@ -207,8 +207,7 @@ def decode(q, k, v, *, n_kv: int, kv_len: int, sinks=None, window: int = 0, ring
     if out is None:
         out = torch.empty_like(q)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
-        # zero-filled once: the in-kernel combine's counters start at 0
-        workspace = torch.zeros(need, dtype=torch.uint8, device=q.device)
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     if sinks is not None:
         assert sinks.dtype == torch.float32 and sinks.is_cuda and sinks.numel() == n_head
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()

@@ -93,9 +93,10 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
     const long long groups = (long long)d->n_seq * d->n_kv * n_rg;
     const long long blocks = (long long)ceil_div(span, 64) * groups;
     // 64-key blocks per wave: enough waves to keep ~8 per CU streaming
-    // one round of resident waves: 256 CUs x 4 SIMDs x the kernel's waves per SIMD
-    const int occ = (d->hd == 64 && rt <= 2) ? 2 : 1;
-    const int target_waves = std::max(64, env_int("PELICA_ATTN_DECODE_WAVES", 1024 * occ));
+    // about one wave per SIMD's worth of splits (256 CUs x 4 SIMDs): each
+    // wave then streams several blocks, and the split count (and the
+    // combine's work) stays small
+    const int target_waves = std::max(64, env_int("PELICA_ATTN_DECODE_WAVES", 1024));
     int spw = env_int("PELICA_ATTN_SPLIT_BLOCKS", 0);
     if (spw <= 0) spw = (int)std::max<long long>(1, (blocks + target_waves - 1) / target_waves);
     long long split_keys = 64LL * pelica::kDecodeWaves * spw;
@@ -111,9 +112,9 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
     pl->n_rg = n_rg;
     pl->split_keys = (int)split_keys;
     pl->n_slot = n_slot;
-    // workspace: arrival counters, (max, sum) pairs, O rows; 256-byte aligned parts
+    // workspace: (max, sum) pairs, then O rows, 256-byte aligned parts
     const size_t n_part = (size_t)d->n_seq * d->n_kv * R * n_slot;
-    pl->ctr_bytes = ((size_t)groups * 4 + 255) & ~(size_t)255;
+    pl->ctr_bytes = 0;
     pl->ml_bytes = (n_part * 2 * 4 + 255) & ~(size_t)255;
     pl->ws_bytes = n_slot > 1 ? pl->ctr_bytes + pl->ml_bytes + n_part * d->hd * 4 : 0;
     return PELICA_ATTN_OK;
@@ -189,7 +190,6 @@ int pelica_attn_decode(const PelicaAttnDesc* desc, const float* q, const uint16_
     p.sinks = sinks;
     p.out = out;
     char* ws = static_cast<char*>(workspace);
-    p.ws_ctr = pl.ws_bytes ? reinterpret_cast<unsigned*>(ws) : nullptr;
     p.ws_ml = pl.ws_bytes ? reinterpret_cast<float*>(ws + pl.ctr_bytes) : nullptr;
     p.ws_o = pl.ws_bytes ? reinterpret_cast<float*>(ws + pl.ctr_bytes + pl.ml_bytes) : nullptr;
     p.seq_len = desc->seq_kv_len;

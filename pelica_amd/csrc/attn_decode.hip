@@ -20,11 +20,11 @@
 //      split into f16 hi + lo as the B operand, straight from the score
 //      registers (its key order matches the A operand's).
 // The NW wave states merge through LDS into one partial (max, sum, O) per row
-// and split.  The last workgroup of a (sequence, kv head, row group) to
-// finish — an agent-scope atomic counter in the workspace — combines the
-// splits in key order with the head's sink and writes the output, so a
-// decode call is one kernel launch.  A single split writes the output
-// directly.
+// and split; a combine kernel with one 256-thread workgroup per query row
+// merges the splits in key order with the head's sink.  (A one-kernel
+// version, where the last workgroup to arrive combines, was measured slower:
+// every split's arrival is a device-scope atomic on one counter, and those
+// serialize.)  A single split writes the output directly.
 //
 // Reference semantics: src/moe_kernels.rs:482-617 (attn_dec, merge_dec),
 // src/oss_batch.rs:172-251 (ATTN_T: window, ring, sink), :253-425 (attn_s +
@@ -45,21 +45,6 @@ __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
     return x;
-}
-
-// Partials cross workgroups (and XCDs, whose L2s are not coherent with each
-// other) through agent-scope atomic accesses: these write through to / read
-// from the device-coherent level, so no L2 writeback or invalidate of the
-// whole cache is needed around the arrival counter.
-__device__ __forceinline__ void store_coherent(float* p, float a, float b) {
-    const uint64_t v = (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(b) << 32);
-    __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ float2 load_coherent(const float* p) {
-    const uint64_t v =
-        __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
 }
 
 // waves per SIMD the decode kernel is compiled for (register budget 512/n)
@@ -119,12 +104,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     constexpr int NP = kDecodeSplitParts;              // f16 parts of Q and P (hi, lo)
     constexpr int VBUF = 64 * HD * 2;                  // bytes of one wave's V block
     constexpr int MERGE = NW * ROWS * (HD + 2) * 4;    // bytes of the wave-merge area
-    // bytes of the split combine: weights, 1/sum, per-phase partial sums
-    constexpr int WTS = (ROWS * kMaxSlots + ROWS) * 4 + 64 * NW * 16;
-    constexpr int SMEM1 = VBUF * NW > MERGE ? VBUF * NW : MERGE;
-    constexpr int SMEM = SMEM1 > WTS ? SMEM1 : WTS;
+    constexpr int SMEM = VBUF * NW > MERGE ? VBUF * NW : MERGE;
     __shared__ __attribute__((aligned(16))) char smem[SMEM];
-    __shared__ int s_last;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
     const int kvh = blockIdx.y % p.n_kv, rg = blockIdx.y / p.n_kv;
@@ -367,7 +348,6 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     __syncthreads();
 
     const int rows_here = min(ROWS, p.R - rbase);
-    const size_t grp = (size_t)(s * p.n_kv + kvh) * p.n_rg + rg;
     // (row, 4-dim chunk) items of the workgroup's result
     constexpr int D4 = HD / 4;
     for (int it = tid; it < rows_here * D4; it += 64 * NW) {
@@ -400,105 +380,105 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
             *reinterpret_cast<float4v*>(p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + d) = O * f;
         } else {
             const size_t idx = ((size_t)(s * p.n_kv + kvh) * p.R + r) * p.n_slot + slot;
-            if (d == 0) store_coherent(p.ws_ml + 2 * idx, M, L);
-            store_coherent(p.ws_o + idx * HD + d, O[0], O[1]);
-            store_coherent(p.ws_o + idx * HD + d + 2, O[2], O[3]);
+            if (d == 0) *reinterpret_cast<float2*>(p.ws_ml + 2 * idx) = make_float2(M, L);
+            *reinterpret_cast<float4v*>(p.ws_o + idx * HD + d) = O;
         }
     }
-    if (n_active == 1) return;
+}
 
-    // ---- last workgroup of the group combines the splits ----
-    // the coherent partial stores are complete before the arrival counts
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned old = __hip_atomic_fetch_add(p.ws_ctr + grp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (old == (unsigned)n_active - 1);
+// Combine of the split partials of one query row, in key order, with the
+// head's sink (merge_dec, src/moe_kernels.rs:585-617; ATTN_M,
+// src/oss_batch.rs:395-425).  Grid (R, n_kv, n_seq), 256 threads: thread
+// (phase, 4-dim chunk) sums the splits c = phase (mod phases); the O loads
+// are issued before the (max, sum) pass so both are in flight together.
+template <int HD>
+__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
+    constexpr int D4 = HD / 4;
+    constexpr int PH = 256 / D4;        // phases: 16 (hd 64) or 8 (hd 128)
+    constexpr int J = 16;               // splits per thread per pass
+    __shared__ float s_w[kMaxSlots];
+    __shared__ float s_red[256 / 64];
+    __shared__ float4v s_o[256];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
+    const int len = p.seq_len ? p.seq_len[s] : p.kv_len;
+    if (len < p.T || len <= 0) return;
+    const int lo_min = key_range(len, p.T, 0, p.window).lo;
+    const int split0 = lo_min / p.split_keys;
+    const int n_active = min(p.n_slot, (len - 1) / p.split_keys - split0 + 1);
+    if (n_active <= 1) return;  // the split kernel wrote the output
+    const int t = r / p.hpk, h = kvh * p.hpk + r % p.hpk;
+    const KeyRange krg = key_range(len, p.T, t, p.window);
+    const int c0 = krg.lo / p.split_keys - split0, c1 = min(krg.pos / p.split_keys - split0, n_active - 1);
+    const size_t base = ((size_t)(s * p.n_kv + kvh) * p.R + r) * p.n_slot;
+    const int ph = tid / D4, d = 4 * (tid % D4);
+
+    // first pass of O loads, in flight while the weights are computed
+    float4v ov[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int c = c0 + ph + PH * j;
+        ov[j] = c <= c1 ? *reinterpret_cast<const float4v*>(p.ws_o + (base + c) * HD + d) : float4v{0.f, 0.f, 0.f, 0.f};
     }
-    __syncthreads();
-    if (!s_last) return;
-    float* wts = reinterpret_cast<float*>(smem);               // [ROWS][kMaxSlots] weights
-    float* inv = wts + ROWS * kMaxSlots;                        // [ROWS] 1/L
-    float4v* red = reinterpret_cast<float4v*>(inv + ROWS);     // [phases][pairs] partial sums
-    // per row (one wave each): max over its splits, weights, denominator
-    constexpr int SPL = kMaxSlots / 64;  // splits per lane
-    for (int row = wave; row < rows_here; row += NW) {
-        const int r = rbase + row;
-        const int t = r / p.hpk, h = kvh * p.hpk + r % p.hpk;
-        const KeyRange krg = key_range(len, p.T, t, p.window);
-        const int c0 = krg.lo / p.split_keys - split0, c1 = krg.pos / p.split_keys - split0;
-        const size_t base = ((size_t)(s * p.n_kv + kvh) * p.R + r) * p.n_slot;
-        const float sk = p.sinks ? p.sinks[h] * kLog2e : -INFINITY;
-        float2 ml[SPL];
-        float M = sk;
+    // (max, sum) of the row's splits, read once into registers
+    constexpr int MLJ = kMaxSlots / 256;
+    float2 ml[MLJ];
 #pragma unroll
-        for (int j = 0; j < SPL; ++j) {
-            const int c = lane + 64 * j;
-            ml[j] = (c >= c0 && c <= c1) ? load_coherent(p.ws_ml + 2 * (base + c)) : make_float2(-INFINITY, 0.f);
-            M = fmaxf(M, ml[j].x);
-        }
-        M = wave_max(M);
-        const float ms = (M == -INFINITY) ? 0.f : M;
-        float L = 0.f;
-#pragma unroll
-        for (int j = 0; j < SPL; ++j) {
-            const int c = lane + 64 * j;
-            const float wc = fast_exp2(ml[j].x - ms);
-            L += ml[j].y * wc;
-            wts[row * kMaxSlots + c] = wc;
-        }
-        L = wave_sum(L);
-        if (p.sinks) L += fast_exp2(sk - ms);
-        if (lane == 0) inv[row] = 1.f / L;
+    for (int j = 0; j < MLJ; ++j) {
+        const int c = c0 + tid + 256 * j;
+        ml[j] = c <= c1 ? *reinterpret_cast<const float2*>(p.ws_ml + 2 * (base + c)) : make_float2(-INFINITY, 0.f);
     }
+    const float sk = p.sinks ? p.sinks[h] * kLog2e : -INFINITY;
+    float M = sk;
+#pragma unroll
+    for (int j = 0; j < MLJ; ++j) M = fmaxf(M, ml[j].x);
+    M = wave_max(M);
+    if (lane == 0) s_red[wave] = M;
     __syncthreads();
-    // O: each (row, 4-dim chunk) pair is summed over the splits by `phases`
-    // threads (split c goes to phase c % phases), then the phases in order
-    const int pairs = rows_here * D4;
-    const int phases = max(1, (64 * NW) / pairs);
-    for (int pr0 = 0; pr0 < pairs; pr0 += 64 * NW) {
-        const int pr = pr0 + tid % min(pairs - pr0, 64 * NW);
-        const int ph = pairs - pr0 >= 64 * NW ? 0 : tid / (pairs - pr0);
-        float4v acc = {0.f, 0.f, 0.f, 0.f};
-        if (ph < phases) {
-            const int row = pr / D4, d = 4 * (pr % D4);
-            const size_t base = ((size_t)(s * p.n_kv + kvh) * p.R + rbase + row) * p.n_slot;
-            const float* w = wts + row * kMaxSlots;
-            // 16 splits' loads in flight at once per pass
-            for (int c0 = ph; c0 < n_active; c0 += 16 * phases) {
-                float2 a[16], b[16];
+    M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    const float ms = (M == -INFINITY) ? 0.f : M;
+    float L = 0.f;
 #pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    const int c = c0 + j * phases;
-                    if (c < n_active) {
-                        a[j] = load_coherent(p.ws_o + (base + c) * HD + d);
-                        b[j] = load_coherent(p.ws_o + (base + c) * HD + d + 2);
-                    } else {
-                        a[j] = b[j] = make_float2(0.f, 0.f);
-                    }
-                }
-#pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    const int c = c0 + j * phases;
-                    const float wc = c < n_active ? w[c] : 0.f;
-                    acc += float4v{a[j].x, a[j].y, b[j].x, b[j].y} * wc;
-                }
-            }
-            red[ph * min(pairs - pr0, 64 * NW) + (pr - pr0)] = acc;
-        }
-        __syncthreads();
-        if (tid < min(pairs - pr0, 64 * NW)) {
-            const int prr = pr0 + tid;
-            const int row = prr / D4, d = 4 * (prr % D4);
-            const int r = rbase + row;
-            const int t = r / p.hpk, h = kvh * p.hpk + r % p.hpk;
-            float4v sum = red[tid];
-            for (int q = 1; q < phases; ++q) sum += red[q * min(pairs - pr0, 64 * NW) + tid];
-            *reinterpret_cast<float4v*>(p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + d) = sum * inv[row];
-        }
-        __syncthreads();
+    for (int j = 0; j < MLJ; ++j) {
+        const int c = c0 + tid + 256 * j;
+        const float wc = fast_exp2(ml[j].x - ms);
+        if (c <= c1) s_w[c - c0] = wc;
+        L += ml[j].y * wc;
     }
-    if (tid == 0) __hip_atomic_store(p.ws_ctr + grp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    L = wave_sum(L);
+    __syncthreads();
+    if (lane == 0) s_red[wave] = L;
+    __syncthreads();
+    L = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+    if (p.sinks) L += fast_exp2(sk - ms);
+
+    float4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int c = c0 + ph + PH * j;
+        if (c <= c1) acc += ov[j] * s_w[c - c0];
+    }
+    for (int cb = c0 + PH * J; cb <= c1; cb += PH * J) {
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int c = cb + ph + PH * j;
+            ov[j] = c <= c1 ? *reinterpret_cast<const float4v*>(p.ws_o + (base + c) * HD + d) : float4v{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int c = cb + ph + PH * j;
+            if (c <= c1) acc += ov[j] * s_w[c - c0];
+        }
+    }
+    // the phases in order
+    s_o[tid] = acc;
+    __syncthreads();
+    if (tid < D4) {
+        float4v sum = s_o[tid];
+#pragma unroll
+        for (int q = 1; q < PH; ++q) sum += s_o[q * D4 + tid];
+        *reinterpret_cast<float4v*>(p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + d) = sum * (1.f / L);
+    }
 }
 
 template <int HD, int RT, int NW>
@@ -507,6 +487,9 @@ static hipError_t launch_k(const DecodeParams& p, hipStream_t st) {
     constexpr int D = kDecodeDepth<HD, RT>;
     if (p.ring_cap) hipLaunchKernelGGL((decode_kernel<HD, RT, NW, true, D>), grid, dim3(64 * NW), 0, st, p);
     else hipLaunchKernelGGL((decode_kernel<HD, RT, NW, false, D>), grid, dim3(64 * NW), 0, st, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || p.n_slot == 1) return e;
+    hipLaunchKernelGGL((decode_combine_kernel<HD>), dim3(p.R, p.n_kv, p.n_seq), dim3(256), 0, st, p);
     return hipGetLastError();
 }
 

@@ -4,9 +4,9 @@
 
 namespace pelica {
 
-// most key splits one (sequence, kv head, row group) may have: the last
-// workgroup stages one weight per split and row in LDS
-constexpr int kMaxSlots = 256;
+// most key splits one query row may have (the combine stages one weight per
+// split in LDS)
+constexpr int kMaxSlots = 1024;
 // waves per decode workgroup
 constexpr int kDecodeWaves = 4;
 
@@ -16,7 +16,6 @@ struct DecodeParams {
     const uint16_t* v;
     const float* sinks;
     float* out;
-    unsigned* ws_ctr;  // [n_seq][n_kv][n_rg] arrival counters, zero between calls
     float* ws_ml;      // [n_seq][n_kv][R][n_slot] x (max, sum), base-2 max
     float* ws_o;       // [n_seq][n_kv][R][n_slot][hd]
     const int32_t* seq_len;

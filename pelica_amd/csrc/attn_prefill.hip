@@ -4,19 +4,21 @@
 // Work split.  A workgroup (NW waves) owns one kv head of one sequence and a
 // block of consecutive prompt tokens; its query rows are (token, head) pairs
 // of that kv head's GQA group, so each K/V tile staged in LDS serves every
-// head of the group.  Each wave holds RT tiles of 16 rows.  Keys stream in
-// 64-key tiles, double-buffered in LDS (global loads of tile j+1 are in
-// flight while tile j is computed).
+// head of the group.  Each wave holds RT tiles of 32 rows.  Keys stream in
+// 64-key tiles, double-buffered in LDS: the next tile's global loads are in
+// flight while the current one is computed.
 //
-// Per tile and wave:
-//   S^T[key][row] = K Q^T  — v_mfma_f32_16x16x32_f16, K from LDS (ds_read_b128
-//                            in the A-operand layout), Q resident in VGPRs;
+// Per tile and wave, on v_mfma_f32_32x32x16_f16:
+//   S^T[key][row] = K Q^T — K read from LDS (ds_read_b128, XOR-swizzled rows)
+//     in the A-operand layout, Q resident in VGPRs as the B operand.  A lane
+//     then holds 32 scores of ONE query row (column l%32), so the row max is
+//     an in-lane max plus one permlane32 swap;
 //   softmax in base 2 with a lazy running max: the max moves (and O, l are
-//   rescaled) only when some row's tile max exceeds it by more than 2^8, so
-//   most tiles skip the rescale;  masking (causal, window) only on the tiles
-//   that straddle a boundary;
-//   O^T[dim][row] += V^T P^T — V read from LDS with ds_read_b64_tr_b16 into the
-//   A operand, P (f16) as the B operand straight from the score registers.
+//     rescaled) only when some row's tile max exceeds it by more than 2^8;
+//     masking (causal, window) only on the tiles that straddle a boundary;
+//   O^T[dim][row] += V^T P^T — V read from LDS with ds_read_b64_tr_b16 into
+//     the A operand; P (f16) is the B operand straight from the score
+//     registers: 8 consecutive accumulator elements are one operand.
 // Sinks seed the running state (max = sink, sum = 1), as attn_p does
 // (src/oss_prefill.rs:391-526); the window mask is j > pos || j + win <= pos
 // (src/oss_prefill.rs:408).  Workgroups are ordered so that each XCD works on
@@ -26,16 +28,48 @@
 
 namespace pelica {
 
+typedef float float16v __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ float16v mfma32(const half8& a, const half8& b, const float16v& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// max / sum with the lane 32 apart
+__device__ __forceinline__ float half_max(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float half_sum(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// LDS byte offset of 16-byte piece p of key row k in a K tile: 16-byte pieces
+// XOR-swizzled by the key so the A-operand reads (32 consecutive keys, one
+// piece each) spread over all banks.
+template <int HD>
+__device__ __forceinline__ int k_slot(int k, int p) {
+    return k * (HD * 2) + ((p ^ (k & 7)) << 4);
+}
+
+// ... and in a V tile: swizzled so the transposed reads of 4 consecutive
+// keys at 16 dims hit distinct banks.
+template <int HD>
+__device__ __forceinline__ int v_slot(int k, int p) {
+    return k * (HD * 2) + ((p ^ ((k & 3) << 1)) << 4);
+}
+
 template <int HD, int RT, int NW>
-__global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillParams p, int n_tb, int TB) {
-    constexpr int DS = HD / 32;
-    constexpr int DT = HD / 16;
-    constexpr int KP = HD + 8;                  // LDS row pitch (halfs)
-    constexpr int PIECES = 64 * HD / 8;         // 16-byte pieces per 64-key tile
-    constexpr int PPT = PIECES / (64 * NW);     // pieces per thread (K, and V)
-    static_assert(PIECES % (64 * NW) == 0, "tile pieces must split evenly");
-    __shared__ __attribute__((aligned(16))) _Float16 ks[2][64 * KP];
-    __shared__ __attribute__((aligned(16))) _Float16 vs[2][64 * KP];
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(
+    PrefillParams p, int n_tb, int TB) {
+    constexpr int KS = HD / 16;                 // 16-dim k-steps of QK^T
+    constexpr int DT = HD / 32;                 // 32-dim output tiles
+    constexpr int TILE = 64 * HD * 2;           // bytes of a K (or V) tile
+    constexpr int PPR = HD / 8;                 // 16-byte pieces per key row
+    constexpr int PPT = 64 * PPR / (64 * NW);   // pieces per thread (K, and V)
+    static_assert((64 * PPR) % (64 * NW) == 0, "tile pieces must split evenly");
+    __shared__ __attribute__((aligned(16))) char lds[4 * TILE];  // K0 V0 K1 V1
 
     // XCD-aware block order: dispatch goes round-robin over the 8 XCDs, so
     // give each XCD a contiguous range of logical blocks (same kv head)
@@ -46,7 +80,7 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillParams p, int n
     const int rest = bid / n_tb;
     const int kvh = rest % p.n_kv, s = rest / p.n_kv;
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h2 = lane >> 5, c32 = lane & 31;
     const int len = p.seq_len ? p.seq_len[s] : p.kv_len;
     if (len < p.T || len <= 0) return;
     const int64_t row0 = p.seq_off ? p.seq_off[s] : (int64_t)s * (p.ring_cap ? p.ring_cap : p.kv_len);
@@ -57,76 +91,73 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillParams p, int n
     const int lo_first = (p.window > 0 && pos_first + 1 > p.window) ? pos_first + 1 - p.window : 0;
     const int lo_last = (p.window > 0 && pos_last + 1 > p.window) ? pos_last + 1 - p.window : 0;
 
-    // this lane's rows: Q as B operand, position and window start
-    half8 qb[RT][DS];
-    int posr[RT], lor[RT];
-    bool valid[RT];
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-        const int r = (wave * RT + rt) * 16 + c16;
-        const int t = t0 + r / p.hpk;
-        valid[rt] = r < TB * p.hpk && t < t1;
-        if (valid[rt]) {
-            const int h = kvh * p.hpk + r % p.hpk;
-            const uint16_t* qp = p.q + ((size_t)(s * p.T + t) * p.n_head + h) * HD + 8 * g;
-#pragma unroll
-            for (int ds = 0; ds < DS; ++ds) qb[rt][ds] = load16(qp + 32 * ds);
-            posr[rt] = len - p.T + t;
-            lor[rt] = (p.window > 0 && posr[rt] + 1 > p.window) ? posr[rt] + 1 - p.window : 0;
-        } else {
-#pragma unroll
-            for (int ds = 0; ds < DS; ++ds)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) qb[rt][ds][j] = 0;
-            posr[rt] = -1;
-            lor[rt] = 0;
-        }
-    }
-
-    // running state; a sink starts it at (max = sink, sum = 1)
-    float m[RT], l[RT];
-    float4v o[DT][RT];
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-        m[rt] = -INFINITY;
-        l[rt] = 0.f;
-        if (p.sinks && valid[rt]) {
-            const int r = (wave * RT + rt) * 16 + c16;
-            m[rt] = p.sinks[kvh * p.hpk + r % p.hpk] * kLog2e;
-            l[rt] = g == 0 ? 1.f : 0.f;
-        }
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) o[dt][rt] = float4v{0.f, 0.f, 0.f, 0.f};
-    }
-
+    // K/V tile loads: thread piece i*64*NW + tid -> key, piece
     const uint16_t* kbase = p.k + (size_t)kvh * HD;
     const uint16_t* vbase = p.v + (size_t)kvh * HD;
     const int kb0 = lo_first & ~63;
     const int n_tiles = (pos_last - kb0) / 64 + 1;
-
     u32x4 kr[PPT], vr[PPT];
     auto load_tile = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
             const int piece = i * 64 * NW + tid;
-            const int key = piece / (HD / 8), col = piece % (HD / 8);
-            int j = min(kb + key, len - 1);
+            const int key = piece / PPR, col = piece % PPR;
+            const int j = min(kb + key, len - 1);
             const int64_t row = row0 + (p.ring_cap ? j % p.ring_cap : j);
             kr[i] = *reinterpret_cast<const u32x4*>(kbase + row * p.row_stride + 8 * col);
             vr[i] = *reinterpret_cast<const u32x4*>(vbase + row * p.row_stride + 8 * col);
         }
     };
     auto store_tile = [&](int buf) {
+        char* kt = lds + buf * 2 * TILE;
+        char* vt = kt + TILE;
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
             const int piece = i * 64 * NW + tid;
-            const int key = piece / (HD / 8), col = piece % (HD / 8);
-            *reinterpret_cast<u32x4*>(&ks[buf][key * KP + 8 * col]) = kr[i];
-            *reinterpret_cast<u32x4*>(&vs[buf][key * KP + 8 * col]) = vr[i];
+            const int key = piece / PPR, col = piece % PPR;
+            *reinterpret_cast<u32x4*>(kt + k_slot<HD>(key, col)) = kr[i];
+            *reinterpret_cast<u32x4*>(vt + v_slot<HD>(key, col)) = vr[i];
         }
     };
-
     load_tile(kb0);
+
+    // this lane's query rows (column c32 of each 32-row tile): Q as the B
+    // operand, position and window start
+    half8 qb[RT][KS];
+    int posr[RT], lor[RT];
+    bool valid[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const int r = (wave * RT + rt) * 32 + c32;
+        const int t = t0 + r / p.hpk;
+        valid[rt] = r < TB * p.hpk && t < t1;
+        const int h = kvh * p.hpk + r % p.hpk;
+        const uint16_t* qp = p.q + ((size_t)(s * p.T + (valid[rt] ? t : t0)) * p.n_head + (valid[rt] ? h : 0)) * HD + 8 * h2;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            qb[rt][ks] = load16(qp + 16 * ks);
+            if (!valid[rt]) qb[rt][ks] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+        posr[rt] = valid[rt] ? len - p.T + t : -1;
+        lor[rt] = (p.window > 0 && posr[rt] + 1 > p.window) ? posr[rt] + 1 - p.window : 0;
+    }
+
+    // running state; a sink starts it at (max = sink, sum = 1)
+    float m[RT], l[RT];
+    float16v o[DT][RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        m[rt] = -INFINITY;
+        l[rt] = 0.f;
+        if (p.sinks && valid[rt]) {
+            const int r = (wave * RT + rt) * 32 + c32;
+            m[rt] = p.sinks[kvh * p.hpk + r % p.hpk] * kLog2e;
+            l[rt] = h2 == 0 ? 1.f : 0.f;
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[dt][rt] = float16v{};
+    }
+
     store_tile(0);
     __syncthreads();
 
@@ -135,34 +166,35 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillParams p, int n
         const int buf = it & 1;
         const bool more = it + 1 < n_tiles;
         if (more) load_tile(kb + 64);
+        const char* kt_lds = lds + buf * 2 * TILE;
+        const char* vt_lds = kt_lds + TILE;
 
-        const _Float16* kt_lds = ks[buf];
-        const _Float16* vt_lds = vs[buf];
-
-        // S^T = K Q^T
-        float4v sc[4][RT];
+        // S^T = K Q^T: 2 key tiles x RT row tiles, k-steps outermost
+        float16v sc[2][RT];
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-            half8 ka[DS];
+        for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-            for (int ds = 0; ds < DS; ++ds)
-                ka[ds] = *reinterpret_cast<const half8*>(kt_lds + (16 * kt + c16) * KP + 32 * ds + 8 * g);
+            for (int rt = 0; rt < RT; ++rt) sc[kt][rt] = float16v{};
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt) {
-                float4v acc = {0.f, 0.f, 0.f, 0.f};
+        for (int ks = 0; ks < KS; ++ks) {
+            half8 ka[2];
 #pragma unroll
-                for (int ds = 0; ds < DS; ++ds) acc = mfma16(ka[ds], qb[rt][ds], acc);
-                sc[kt][rt] = acc;
-            }
+            for (int kt = 0; kt < 2; ++kt)
+                ka[kt] = *reinterpret_cast<const half8*>(kt_lds + k_slot<HD>(32 * kt + c32, 2 * ks + h2));
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) sc[kt][rt] = mfma32(ka[kt], qb[rt][ks], sc[kt][rt]);
         }
 
-        // boundary tiles: causal / window mask
+        // boundary tiles only: causal / window mask.  Element i of key tile
+        // kt is key kb + 32 kt + 8 (i / 4) + 4 h2 + i % 4.
         if (kb + 63 > pos_first || kb < lo_last) {
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
+            for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int key = kb + 16 * kt + 4 * g + i;
+                for (int i = 0; i < 16; ++i) {
+                    const int key = kb + 32 * kt + 8 * (i / 4) + 4 * h2 + (i % 4);
 #pragma unroll
                     for (int rt = 0; rt < RT; ++rt)
                         if (key < lor[rt] || key > posr[rt]) sc[kt][rt][i] = -INFINITY;
@@ -176,10 +208,10 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillParams p, int n
         for (int rt = 0; rt < RT; ++rt) {
             float x = -INFINITY;
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
+            for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) x = fmaxf(x, sc[kt][rt][i]);
-            bm[rt] = group4_max(x) * p.qscale;
+                for (int i = 0; i < 16; ++i) x = fmaxf(x, sc[kt][rt][i]);
+            bm[rt] = half_max(x) * p.qscale;
             grow |= bm[rt] > m[rt] + 8.f;
         }
         if (__builtin_amdgcn_ballot_w64(grow)) {
@@ -196,57 +228,71 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillParams p, int n
             }
         }
 
-        half8 pb[RT][2];
+        // P = 2^(s*scale - m) as f16 B operands; chunk u (16 keys) is
+        // elements 8(u%2) .. +7 of key tile u/2
+        half8 pb[4][RT];
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
             const float ms = (m[rt] == -INFINITY) ? 0.f : m[rt];
             float ls = 0.f;
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
+            for (int u = 0; u < 4; ++u)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float pe = fast_exp2(__builtin_fmaf(sc[kt][rt][i], p.qscale, -ms));
+                for (int j = 0; j < 8; ++j) {
+                    const float pe = fast_exp2(__builtin_fmaf(sc[u >> 1][rt][8 * (u & 1) + j], p.qscale, -ms));
                     ls += pe;
-                    pb[rt][kt >> 1][(kt & 1) * 4 + i] = (_Float16)pe;
+                    pb[u][rt][j] = (_Float16)pe;
                 }
             l[rt] += ls;
         }
 
         // O^T += V^T P^T
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
+        for (int u = 0; u < 4; ++u) {
+            half8 va[DT];
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const _Float16* a = vt_lds + (32 * u + 4 * g + (c16 >> 2)) * KP + 16 * dt + 4 * (c16 & 3);
-                const half8 va = cat8(lds_read_tr(a), lds_read_tr(a + 16 * KP));
-#pragma unroll
-                for (int rt = 0; rt < RT; ++rt) o[dt][rt] = mfma16(va, pb[rt][u], o[dt][rt]);
+            for (int dt = 0; dt < DT; ++dt) {
+                // lanes of 16-lane group G read keys 16u + 4 h2 + r (+8) at
+                // dims 32 dt + 16 (G & 1) + 4 q; lane 4r + q of the group
+                const int G = lane >> 4, r4 = (lane & 15) >> 2, q4 = lane & 3;
+                const int key = 16 * u + 4 * h2 + r4, dim = 32 * dt + 16 * (G & 1) + 4 * q4;
+                const _Float16* a0 = reinterpret_cast<const _Float16*>(vt_lds + v_slot<HD>(key, dim >> 3) + ((dim & 7) << 1));
+                const _Float16* a1 = reinterpret_cast<const _Float16*>(vt_lds + v_slot<HD>(key + 8, dim >> 3) + ((dim & 7) << 1));
+                va[dt] = cat8(lds_read_tr(a0), lds_read_tr(a1));
             }
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) o[dt][rt] = mfma32(va[dt], pb[u][rt], o[dt][rt]);
+        }
 
         if (more) store_tile(buf ^ 1);
         __syncthreads();
     }
 
+    // O^T lane layout: dim 32 dt + 8 (i / 4) + 4 h2 + i % 4 of row c32
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-        const float lt = group4_sum(l[rt]);
+        const float lt = half_sum(l[rt]);
         if (!valid[rt]) continue;
-        const int r = (wave * RT + rt) * 16 + c16;
+        const int r = (wave * RT + rt) * 32 + c32;
         const int t = t0 + r / p.hpk, h = kvh * p.hpk + r % p.hpk;
         const float inv = 1.f / lt;
-        uint16_t* op = p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + 4 * g;
+        uint16_t* op = p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + 4 * h2;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-            const half4 hv = {(_Float16)(o[dt][rt][0] * inv), (_Float16)(o[dt][rt][1] * inv),
-                              (_Float16)(o[dt][rt][2] * inv), (_Float16)(o[dt][rt][3] * inv)};
-            *reinterpret_cast<half4*>(op + 16 * dt) = hv;
-        }
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                const half4 hv = {(_Float16)(o[dt][rt][4 * i4] * inv), (_Float16)(o[dt][rt][4 * i4 + 1] * inv),
+                                  (_Float16)(o[dt][rt][4 * i4 + 2] * inv), (_Float16)(o[dt][rt][4 * i4 + 3] * inv)};
+                *reinterpret_cast<half4*>(op + 32 * dt + 8 * i4) = hv;
+            }
     }
 }
 
 template <int HD, int RT, int NW>
 static hipError_t launch(const PrefillParams& p, hipStream_t st) {
-    constexpr int ROWS = NW * RT * 16;
+    constexpr int ROWS = NW * RT * 32;
     if (p.hpk > ROWS) return hipErrorNotSupported;
     const int TB = ROWS / p.hpk;
     const int n_tb = (p.T + TB - 1) / TB;
@@ -257,8 +303,8 @@ static hipError_t launch(const PrefillParams& p, hipStream_t st) {
 }
 
 hipError_t launch_prefill(const PrefillParams& p, hipStream_t st) {
-    if (p.hd == 64) return launch<64, 4, 4>(p, st);
-    if (p.hd == 128) return launch<128, 2, 4>(p, st);
+    if (p.hd == 64) return launch<64, 2, 4>(p, st);
+    if (p.hd == 128) return launch<128, 1, 4>(p, st);
     return hipErrorNotSupported;
 }
 

@@ -139,9 +139,8 @@ def test_errors_surface_as_exceptions():
     assert e.value.code == attn.EINVAL
 
 
-def test_workspace_reuse_and_counters_reset():
-    # one zero-filled workspace serves repeated calls; the in-kernel combine
-    # leaves its arrival counters at zero after each call
+def test_workspace_reuse():
+    # one workspace (uninitialised contents) serves repeated calls
     from pelica_amd.attn import make_desc, new_workspace
 
     inp = wl.make_inputs(wl.C3_FULL.scaled(kv_len=20000), "cuda")
@@ -151,7 +150,6 @@ def test_workspace_reuse_and_counters_reset():
             for _ in range(3)]
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
-    assert int(ws[:256].view(torch.int32).abs().sum()) == 0
     ref = oracle_run(inp)
     assert_close(as_f64(outs[2]), as_f64(ref), what="reused workspace")
 
@@ -184,6 +182,7 @@ def test_reused_workspace_with_changing_inputs():
 
     desc = make_desc(64, 8, 64, kv_len=30000)
     ws = new_workspace(desc)
+    ws.fill_(0xFF)  # garbage in the workspace is fine
     for seed in (101, 102, 103):
         inp = wl.make_inputs(wl.C3_FULL.scaled(kv_len=30000, seed=seed), "cuda")
         got = attn.decode(inp.q, inp.k, inp.v, n_kv=8, kv_len=30000, sinks=inp.sinks, workspace=ws)
