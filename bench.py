@@ -58,7 +58,8 @@ def time_calls(fn, n_copies, steps, warmup, graph=True):
     torch.cuda.synchronize()
     st = torch.cuda.current_stream()
     if graph:
-        per = max(n_copies, 8 if n_copies == 1 else n_copies)
+        # enough calls per graph to amortise the replay's fixed cost (~20 us)
+        per = n_copies * max(1, -(-64 // n_copies))
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             for i in range(per):

@@ -81,9 +81,9 @@ const char* pelica_attn_last_error(void);
 size_t pelica_attn_workspace_bytes(const PelicaAttnDesc* desc);
 
 /* Zero-fill a workspace on `stream` with a fill kernel (safe to record in a
- * HIP graph).  Decode does not require it; it exists for callers that want
- * deterministic workspace contents.  No counterpart in the reference, whose
- * wgpu buffers start zeroed at creation (src/moe.rs:949-952). */
+ * HIP graph).  Decode does not require it; it is there for callers that
+ * want deterministic workspace contents.  No counterpart in the reference,
+ * whose wgpu buffers start zeroed at creation (src/moe.rs:949-952). */
 int pelica_attn_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
 
 /* Decode attention: f32 queries over the f16 cache, f32 output, split-K

@@ -178,7 +178,7 @@ def workspace_bytes(desc: AttnDesc) -> int:
 
 
 def new_workspace(desc: AttnDesc, device="cuda"):
-    """A workspace for decode calls with this descriptor."""
+    """A workspace for decode calls with this descriptor (no init needed)."""
     import torch
 
     return torch.empty(max(workspace_bytes(desc), 16), dtype=torch.uint8, device=device)

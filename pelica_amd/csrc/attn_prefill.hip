@@ -29,6 +29,10 @@
 namespace pelica {
 
 typedef float float16v __attribute__((ext_vector_type(16)));
+typedef _Float16 half2 __attribute__((ext_vector_type(2)));
+
+// word 3 of a gfx9 buffer resource: 32-bit data format, raw addressing
+constexpr int kBufferFlags = 0x00020000;
 
 __device__ __forceinline__ float16v mfma32(const half8& a, const half8& b, const float16v& c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -60,7 +64,7 @@ __device__ __forceinline__ int v_slot(int k, int p) {
     return k * (HD * 2) + ((p ^ ((k & 3) << 1)) << 4);
 }
 
-template <int HD, int RT, int NW>
+template <int HD, int RT, int NW, bool RING>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(
     PrefillParams p, int n_tb, int TB) {
     constexpr int KS = HD / 16;                 // 16-dim k-steps of QK^T
@@ -91,21 +95,28 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     const int lo_first = (p.window > 0 && pos_first + 1 > p.window) ? pos_first + 1 - p.window : 0;
     const int lo_last = (p.window > 0 && pos_last + 1 > p.window) ? pos_last + 1 - p.window : 0;
 
-    // K/V tile loads: thread piece i*64*NW + tid -> key, piece
-    const uint16_t* kbase = p.k + (size_t)kvh * HD;
-    const uint16_t* vbase = p.v + (size_t)kvh * HD;
+    // K/V tile loads through buffer resources over this sequence's rows of kv
+    // head kvh: 32-bit offsets; rows past the sequence read as 0 (masked)
+    const uint32_t stride_b = (uint32_t)p.row_stride * 2;
+    const uint32_t nrec = (RING ? (uint32_t)p.ring_cap : (uint32_t)len) * stride_b;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.k + row0 * p.row_stride + (size_t)kvh * HD), (short)0, (int)nrec, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.v + row0 * p.row_stride + (size_t)kvh * HD), (short)0, (int)nrec, kBufferFlags);
     const int kb0 = lo_first & ~63;
     const int n_tiles = (pos_last - kb0) / 64 + 1;
+    // thread piece i*64*NW + tid of a tile -> (key, 16-byte column)
+    constexpr int KPI = 64 * NW / PPR;  // keys per piece round
+    const int pkey = tid / PPR, pcol = tid % PPR;
     u32x4 kr[PPT], vr[PPT];
     auto load_tile = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
-            const int piece = i * 64 * NW + tid;
-            const int key = piece / PPR, col = piece % PPR;
-            const int j = min(kb + key, len - 1);
-            const int64_t row = row0 + (p.ring_cap ? j % p.ring_cap : j);
-            kr[i] = *reinterpret_cast<const u32x4*>(kbase + row * p.row_stride + 8 * col);
-            vr[i] = *reinterpret_cast<const u32x4*>(vbase + row * p.row_stride + 8 * col);
+            const int key = KPI * i + pkey;
+            const uint32_t off = RING ? ((kb + key) % p.ring_cap) * stride_b + 16 * pcol
+                                      : (uint32_t)(kb + key) * stride_b + 16 * pcol;
+            kr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+            vr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
         }
     };
     auto store_tile = [&](int buf) {
@@ -113,10 +124,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
         char* vt = kt + TILE;
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
-            const int piece = i * 64 * NW + tid;
-            const int key = piece / PPR, col = piece % PPR;
-            *reinterpret_cast<u32x4*>(kt + k_slot<HD>(key, col)) = kr[i];
-            *reinterpret_cast<u32x4*>(vt + v_slot<HD>(key, col)) = vr[i];
+            const int key = KPI * i + pkey;
+            *reinterpret_cast<u32x4*>(kt + k_slot<HD>(key, pcol)) = kr[i];
+            *reinterpret_cast<u32x4*>(vt + v_slot<HD>(key, pcol)) = vr[i];
         }
     };
     load_tile(kb0);
@@ -230,19 +240,22 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 
         // P = 2^(s*scale - m) as f16 B operands; chunk u (16 keys) is
         // elements 8(u%2) .. +7 of key tile u/2
+        // (the row sum takes the f16 P the PV product uses, two at a time)
         half8 pb[4][RT];
+        const half2 one2 = {(_Float16)1.f, (_Float16)1.f};
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
             const float ms = (m[rt] == -INFINITY) ? 0.f : m[rt];
             float ls = 0.f;
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
+            for (int u = 0; u < 4; ++u) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float pe = fast_exp2(__builtin_fmaf(sc[u >> 1][rt][8 * (u & 1) + j], p.qscale, -ms));
-                    ls += pe;
-                    pb[u][rt][j] = (_Float16)pe;
-                }
+                for (int j = 0; j < 8; ++j)
+                    pb[u][rt][j] = (_Float16)fast_exp2(__builtin_fmaf(sc[u >> 1][rt][8 * (u & 1) + j], p.qscale, -ms));
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    ls = __builtin_amdgcn_fdot2(half2{pb[u][rt][2 * j], pb[u][rt][2 * j + 1]}, one2, ls, false);
+            }
             l[rt] += ls;
         }
 
@@ -298,7 +311,10 @@ static hipError_t launch(const PrefillParams& p, hipStream_t st) {
     const int n_tb = (p.T + TB - 1) / TB;
     const long long nblk = (long long)n_tb * p.n_kv * p.n_seq;
     if (nblk > 0x7fffffff) return hipErrorNotSupported;
-    hipLaunchKernelGGL((prefill_kernel<HD, RT, NW>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p, n_tb, TB);
+    if (p.ring_cap)
+        hipLaunchKernelGGL((prefill_kernel<HD, RT, NW, true>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p, n_tb, TB);
+    else
+        hipLaunchKernelGGL((prefill_kernel<HD, RT, NW, false>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p, n_tb, TB);
     return hipGetLastError();
 }
 

@@ -182,9 +182,16 @@ def test_reused_workspace_with_changing_inputs():
 
     desc = make_desc(64, 8, 64, kv_len=30000)
     ws = new_workspace(desc)
-    ws.fill_(0xFF)  # garbage in the workspace is fine
+    ws.fill_(0xFF)  # garbage contents are fine
     for seed in (101, 102, 103):
         inp = wl.make_inputs(wl.C3_FULL.scaled(kv_len=30000, seed=seed), "cuda")
         got = attn.decode(inp.q, inp.k, inp.v, n_kv=8, kv_len=30000, sinks=inp.sinks, workspace=ws)
         torch.cuda.synchronize()
         assert_close(as_f64(got), as_f64(oracle_run(inp)), what=f"seed {seed}")
+
+
+def test_workspace_init_zero_fills():
+    ws = torch.full((4096,), 0xAB, dtype=torch.uint8, device="cuda")
+    assert attn.load_library().pelica_attn_workspace_init(ws.data_ptr(), ws.numel(), None) == 0
+    torch.cuda.synchronize()
+    assert int(ws.sum()) == 0
