@@ -27,6 +27,12 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
 F16_PEAK_TFLOPS = 2500.0    # MI355X dense f16 MFMA
+# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (KiB per
+# dispatch), FETCH_SIZE scaled by 2.0: on this GPU it reads half the bytes a
+# plain copy of known size moves, while WRITE_SIZE reads them exactly
+# (profiles/hbm_traffic_counters.md).
+HBM_TRAFFIC_C3 = 67_935_949   # 32883.8 KiB fetched (x2) + 576.1 KiB written per split launch
+HBM_TRAFFIC_C4 = 77_239_706   # 21330.7 KiB fetched (x2) + 32768 KiB written per prefill launch
 
 
 def parse():
@@ -36,6 +42,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of config names to time (default: all)")
+    ap.add_argument("--profile", default="",
+                    help="comma list of configs: just run each --steps times, eagerly, for rocprofv3 passes")
     return ap.parse_args()
 
 
@@ -85,6 +93,25 @@ def time_calls(fn, n_copies, steps, warmup, graph=True):
     return e0.elapsed_time(e1) / steps
 
 
+def kernel_times(fn, n_copies, reps):
+    """Average GPU time per kernel kind over `reps` eager calls, from the
+    library's own per-kernel HIP events (pelica_attn_prof_*)."""
+    import torch
+
+    from pelica_amd import attn
+
+    attn.prof_enable(True)
+    for i in range(reps):
+        fn(i % n_copies)
+    torch.cuda.synchronize()
+    recs = attn.prof_read()
+    attn.prof_enable(False)
+    out = {}
+    for name, ms in recs:
+        out.setdefault(name, []).append(ms)
+    return {k: sum(v) / len(v) for k, v in out.items()}
+
+
 def bench_decode(cfg, steps, warmup):
     import torch
 
@@ -109,9 +136,12 @@ def bench_decode(cfg, steps, warmup):
 
     ms = time_calls(call, len(ks), steps, warmup)
     ms_eager = time_calls(call, len(ks), steps, warmup, graph=False)
+    kt = kernel_times(call, len(ks), steps)
     nbytes = wl.kv_bytes(cfg, inp.seq_len.tolist())
     gbs = nbytes / (ms * 1e-3) / 1e9
+    split_ms = kt.get("decode_split", ms)
     return dict(config=cfg.name, ms=ms, ms_eager=ms_eager, bytes=nbytes, GBps=gbs, frac_hbm=gbs / HBM_PEAK_GBS,
+                kernel_ms=kt, split_GBps=nbytes / (split_ms * 1e-3) / 1e9,
                 workspace_bytes=ws_n, kv_copies=len(ks))
 
 
@@ -129,9 +159,12 @@ def bench_prefill(cfg, steps, warmup):
                      out=out)
 
     ms = time_calls(call, 1, steps, warmup)
+    kt = kernel_times(call, 1, steps)
     flops = wl.attn_flops(cfg)
     tf = flops / (ms * 1e-3) / 1e12
-    return dict(config=cfg.name, ms=ms, flops=flops, TFLOPs=tf, frac_mfma=tf / F16_PEAK_TFLOPS)
+    kms = kt.get("prefill", ms)
+    return dict(config=cfg.name, ms=ms, flops=flops, TFLOPs=tf, frac_mfma=tf / F16_PEAK_TFLOPS, kernel_ms=kt,
+                kernel_TFLOPs=flops / (kms * 1e-3) / 1e12)
 
 
 def cpu_baseline_decode(cfg, reps=5):
@@ -183,6 +216,35 @@ def cpu_baseline_prefill(cfg, rows=32):
                 sample=f"last {rows} of {T} prompt tokens of {cfg.name}", ms=sec * 1e3)
 
 
+def profile_only(args):
+    """Run the named configs eagerly (no graphs, no timing) for profilers."""
+    import torch
+
+    from pelica_amd import attn
+    from pelica_amd import workloads as wl
+
+    for name in args.profile.split(","):
+        if name == "copy":  # calibration: a plain 256 MiB device copy
+            x = torch.ones(256 << 20, dtype=torch.uint8, device="cuda")
+            y = torch.empty_like(x)
+            for _ in range(args.steps):
+                y.copy_(x)
+            torch.cuda.synchronize()
+            continue
+        cfg = wl.CONFIGS[name]
+        inp = wl.make_inputs(cfg, "cuda")
+        kw = dict(n_kv=cfg.n_kv, kv_len=inp.kv_len, sinks=inp.sinks, window=cfg.window)
+        if inp.ragged:
+            kw.update(seq_kv_len=inp.seq_len, seq_kv_offset=inp.seq_off)
+        for _ in range(args.steps):
+            if cfg.kind == "decode":
+                attn.decode(inp.q, inp.k, inp.v, **kw)
+            else:
+                attn.prefill(inp.q, inp.k, inp.v, **kw)
+        torch.cuda.synchronize()
+        print(f"profiled {name} x{args.steps}", flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -194,6 +256,8 @@ def main():
     from pelica_amd import workloads as wl
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.profile:
+        return profile_only(args)
     only = set(filter(None, args.only.split(",")))
 
     def want(c):
@@ -233,15 +297,19 @@ def main():
                     for k, r in results.items()},
     }
     if head:
-        line["roofline"] = {"bound": "hbm", "achieved": round(head["GBps"], 1), "peak": HBM_PEAK_GBS,
-                            "unit": "GB/s", "frac": round(head["frac_hbm"], 4), "traffic": None,
-                            "kernel": "decode call (split + combine), HIP events per call"}
+        sg = head["split_GBps"]
+        line["roofline"] = {"bound": "hbm", "achieved": round(sg, 1), "peak": HBM_PEAK_GBS,
+                            "unit": "GB/s", "frac": round(sg / HBM_PEAK_GBS, 4), "traffic": HBM_TRAFFIC_C3,
+                            "kernel": "decode split kernel (decode_kernel<64,1,4>), per-launch HIP events",
+                            "kernel_ms": round(head["kernel_ms"].get("decode_split", float("nan")), 5)}
     if pre:
         line["prefill"] = {"workload": wl.C4_FULL.name, "value": round(pre["TFLOPs"], 1), "unit": "TFLOP/s",
                            "ms_per_step": round(pre["ms"], 5),
-                           "roofline": {"bound": "mfma", "achieved": round(pre["TFLOPs"], 1),
+                           "roofline": {"bound": "mfma", "achieved": round(pre["kernel_TFLOPs"], 1),
                                         "peak": F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                        "frac": round(pre["frac_mfma"], 4), "traffic": None},
+                                        "frac": round(pre["kernel_TFLOPs"] / F16_PEAK_TFLOPS, 4),
+                                        "traffic": HBM_TRAFFIC_C4,
+                                        "kernel_ms": round(pre["kernel_ms"].get("prefill", float("nan")), 5)},
                            "cpu_baseline": cpu_pre}
     print(json.dumps(line), flush=True)
 

@@ -113,6 +113,31 @@ int pelica_attn_partials_merge(int32_t n_head, int32_t hd, int32_t n_parts,
                                const float* parts, const float* sinks, float* out,
                                void* stream);
 
+/* ---- per-kernel GPU timing ------------------------------------------- */
+
+/* kernel ids of PelicaAttnProfRecord */
+#define PELICA_ATTN_PROF_DECODE_SPLIT 1
+#define PELICA_ATTN_PROF_DECODE_COMBINE 2
+#define PELICA_ATTN_PROF_PREFILL 3
+#define PELICA_ATTN_PROF_MERGE 4
+
+typedef struct PelicaAttnProfRecord {
+    int32_t kernel; /* PELICA_ATTN_PROF_* */
+    float ms;       /* GPU time between the events bracketing the launch */
+} PelicaAttnProfRecord;
+
+/* Turn per-kernel timing on (1) or off (0); either way pending records are
+ * dropped.  While on, each kernel launch is bracketed by HIP events on its
+ * stream (launches on a capturing stream are not timed).  Replaces the
+ * reference's PELICA_PROF timestamp queries (src/moe.rs:1761-1833,
+ * src/oss.rs:1164-1242). */
+int pelica_attn_prof_enable(int on);
+
+/* Wait for the recorded launches, copy up to max_records of them (in launch
+ * order) to out and drop all records.  Returns the number copied, or a
+ * negative status. */
+int pelica_attn_prof_read(PelicaAttnProfRecord* out, int max_records);
+
 #ifdef __cplusplus
 }
 #endif

@@ -16,6 +16,8 @@ from .attn import (  # noqa: F401
     new_workspace,
     partials_merge,
     prefill,
+    prof_enable,
+    prof_read,
     workspace_bytes,
 )
 
@@ -29,5 +31,7 @@ __all__ = [
     "new_workspace",
     "partials_merge",
     "prefill",
+    "prof_enable",
+    "prof_read",
     "workspace_bytes",
 ]

@@ -37,7 +37,12 @@ EXPORTS = (
     "pelica_attn_decode",
     "pelica_attn_prefill",
     "pelica_attn_partials_merge",
+    "pelica_attn_prof_enable",
+    "pelica_attn_prof_read",
 )
+
+#: kernel ids of the per-kernel timing records
+PROF_KERNELS = {1: "decode_split", 2: "decode_combine", 3: "prefill", 4: "partials_merge"}
 
 
 class AttnError(RuntimeError):
@@ -64,6 +69,10 @@ class Shape:
     @property
     def n_head(self) -> int:
         return self.n_kv * self.hpk
+
+
+class ProfRecord(ctypes.Structure):
+    _fields_ = [("kernel", ctypes.c_int32), ("ms", ctypes.c_float)]
 
 
 class AttnDesc(ctypes.Structure):
@@ -122,6 +131,10 @@ def load_library() -> ctypes.CDLL:
     lib.pelica_attn_prefill.argtypes = [dp, vp, vp, vp, vp, vp, vp]
     lib.pelica_attn_partials_merge.restype = ctypes.c_int
     lib.pelica_attn_partials_merge.argtypes = [i32, i32, i32, vp, vp, vp, vp]
+    lib.pelica_attn_prof_enable.restype = ctypes.c_int
+    lib.pelica_attn_prof_enable.argtypes = [ctypes.c_int]
+    lib.pelica_attn_prof_read.restype = ctypes.c_int
+    lib.pelica_attn_prof_read.argtypes = [ctypes.POINTER(ProfRecord), ctypes.c_int]
     _lib = lib
     return lib
 
@@ -258,3 +271,17 @@ def partials_merge(parts, *, n_head: int, hd: int, sinks=None, out=None, stream=
 
 def default_scale(hd: int) -> float:
     return 1.0 / math.sqrt(hd)
+
+
+def prof_enable(on: bool = True) -> None:
+    """Per-kernel GPU timing of the library's launches (HIP events)."""
+    _check(load_library().pelica_attn_prof_enable(1 if on else 0))
+
+
+def prof_read(max_records: int = 1 << 14) -> list:
+    """[(kernel name, ms), ...] of the launches timed since the last read."""
+    buf = (ProfRecord * max_records)()
+    n = load_library().pelica_attn_prof_read(buf, max_records)
+    if n < 0:
+        _check(n)
+    return [(PROF_KERNELS.get(buf[i].kernel, str(buf[i].kernel)), buf[i].ms) for i in range(n)]

@@ -9,6 +9,7 @@
 #include "../../include/pelica_attn.h"
 #include "attn_decode.hpp"
 #include "attn_prefill.hpp"
+#include "attn_prof.hpp"
 
 namespace {
 
@@ -253,6 +254,7 @@ int pelica_attn_partials_merge(int32_t n_head, int32_t hd, int32_t n_parts, cons
     if (n_head <= 0 || hd <= 0 || n_parts <= 0)
         return fail(PELICA_ATTN_EINVAL, "n_head %d, hd %d and n_parts %d must be positive", n_head, hd, n_parts);
     if (!parts || !out) return fail(PELICA_ATTN_EINVAL, "parts and out must be non-NULL");
+    pelica::ProfScope ps(pelica::kProfMerge, static_cast<hipStream_t>(stream));
     hipLaunchKernelGGL(partials_merge_kernel, dim3(n_head), dim3(64), 0, static_cast<hipStream_t>(stream), n_head, hd,
                        n_parts, parts, sinks, out);
     hipError_t e = hipGetLastError();

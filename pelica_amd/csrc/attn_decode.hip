@@ -32,6 +32,7 @@
 #include <algorithm>
 
 #include "attn_decode.hpp"
+#include "attn_prof.hpp"
 
 namespace pelica {
 
@@ -485,10 +486,14 @@ template <int HD, int RT, int NW>
 static hipError_t launch_k(const DecodeParams& p, hipStream_t st) {
     dim3 grid(p.n_slot, p.n_kv * p.n_rg, p.n_seq);
     constexpr int D = kDecodeDepth<HD, RT>;
+    {
+    ProfScope ps(kProfDecodeSplit, st);
     if (p.ring_cap) hipLaunchKernelGGL((decode_kernel<HD, RT, NW, true, D>), grid, dim3(64 * NW), 0, st, p);
     else hipLaunchKernelGGL((decode_kernel<HD, RT, NW, false, D>), grid, dim3(64 * NW), 0, st, p);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.n_slot == 1) return e;
+    ProfScope ps(kProfDecodeCombine, st);
     hipLaunchKernelGGL((decode_combine_kernel<HD>), dim3(p.R, p.n_kv, p.n_seq), dim3(256), 0, st, p);
     return hipGetLastError();
 }

@@ -25,6 +25,7 @@
 // one kv head (its K/V stays in that XCD's L2) and the longest key ranges
 // start first.
 #include "attn_prefill.hpp"
+#include "attn_prof.hpp"
 
 namespace pelica {
 
@@ -311,6 +312,7 @@ static hipError_t launch(const PrefillParams& p, hipStream_t st) {
     const int n_tb = (p.T + TB - 1) / TB;
     const long long nblk = (long long)n_tb * p.n_kv * p.n_seq;
     if (nblk > 0x7fffffff) return hipErrorNotSupported;
+    ProfScope ps(kProfPrefill, st);
     if (p.ring_cap)
         hipLaunchKernelGGL((prefill_kernel<HD, RT, NW, true>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p, n_tb, TB);
     else

@@ -195,3 +195,17 @@ def test_workspace_init_zero_fills():
     assert attn.load_library().pelica_attn_workspace_init(ws.data_ptr(), ws.numel(), None) == 0
     torch.cuda.synchronize()
     assert int(ws.sum()) == 0
+
+
+def test_per_kernel_timing():
+    inp = wl.make_inputs(wl.C3_FULL, "cuda")
+    attn.prof_enable(True)
+    for _ in range(3):
+        attn.decode(inp.q, inp.k, inp.v, n_kv=8, kv_len=inp.kv_len, sinks=inp.sinks)
+    torch.cuda.synchronize()
+    recs = attn.prof_read()
+    attn.prof_enable(False)
+    names = [n for n, _ in recs]
+    assert names.count("decode_split") == 3 and names.count("decode_combine") == 3
+    assert all(ms > 0 for _, ms in recs)
+    assert attn.prof_read() == []
