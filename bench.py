@@ -300,7 +300,7 @@ def main():
         sg = head["split_GBps"]
         line["roofline"] = {"bound": "hbm", "achieved": round(sg, 1), "peak": HBM_PEAK_GBS,
                             "unit": "GB/s", "frac": round(sg / HBM_PEAK_GBS, 4), "traffic": HBM_TRAFFIC_C3,
-                            "kernel": "decode split kernel (decode_kernel<64,1,4>), per-launch HIP events",
+                            "kernel": "decode split kernel (decode_kernel<64,1,8,4>), per-launch HIP events",
                             "kernel_ms": round(head["kernel_ms"].get("decode_split", float("nan")), 5)}
     if pre:
         line["prefill"] = {"workload": wl.C4_FULL.name, "value": round(pre["TFLOPs"], 1), "unit": "TFLOP/s",

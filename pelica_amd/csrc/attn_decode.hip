@@ -1,10 +1,15 @@
 // Split-K flash-decode for gfx950: f32 queries, f16 KV cache, f32 output.
 //
-// Work split.  A workgroup of NW waves owns (sequence s, kv head g, row group,
-// key split).  All query rows that share kv head g — the GQA group times the
-// pass's tokens (drafts) — ride in the same wave, so every K/V byte is read
-// from HBM once.  Rows sit in the MFMA's 16-wide n dimension; keys stream
-// through in blocks of 64, the waves of a workgroup taking every NW-th block.
+// Work split.  A workgroup of NW waves owns (sequence s, wg_heads
+// consecutive kv heads, row group, key split): wave w serves kv head
+// w % wg_heads and takes every (NW / wg_heads)-th 64-key block of the split.
+// The waves of the different heads walk the same keys side by side, so each
+// cache row (all kv heads of a position, adjacent in memory) is fetched by
+// one workgroup at one time — on MI355X, spreading a row's head slices over
+// workgroups that reach it at different times costs ~25% of HBM throughput.
+// All query rows that share kv head g — the GQA group times the pass's
+// tokens (drafts) — ride in the same wave, so every K/V byte is read from
+// HBM once.  Rows sit in the MFMA's 16-wide n dimension.
 //
 // Per 64-key block (software-pipelined one block ahead):
 //   K  global -> registers with 128-bit loads, directly in the A-operand
@@ -19,8 +24,8 @@
 //      transposing ds_read_b64_tr_b16 as the A operand of O^T = V^T P^T; P is
 //      split into f16 hi + lo as the B operand, straight from the score
 //      registers (its key order matches the A operand's).
-// The NW wave states merge through LDS into one partial (max, sum, O) per row
-// and split; a combine kernel with one 256-thread workgroup per query row
+// The wave states of each head merge through LDS into one partial (max, sum,
+// O) per row and split; a combine kernel with one 256-thread workgroup per query row
 // merges the splits in key order with the head's sink.  (A one-kernel
 // version, where the last workgroup to arrive combines, was measured slower:
 // every split's arrival is a device-scope atomic on one counter, and those
@@ -48,15 +53,12 @@ __device__ __forceinline__ float wave_sum(float x) {
     return x;
 }
 
-// waves per SIMD the decode kernel is compiled for (register budget 512/n)
-template <int HD, int RT>
-#ifndef PELICA_OCC64
-#define PELICA_OCC64 3
-#endif
 #ifndef PELICA_DEPTH64
 #define PELICA_DEPTH64 1
 #endif
-constexpr int kDecodeOcc = HD == 64 ? (RT == 1 ? PELICA_OCC64 : RT == 2 ? 2 : 1) : 1;
+// waves per SIMD the decode kernel is compiled for (register budget 512/n)
+template <int HD, int RT, int NW>
+constexpr int kDecodeOcc = NW == 8 ? 2 : HD == 64 ? (RT == 1 ? 3 : RT == 2 ? 2 : 1) : 1;
 
 // f16 parts the decode kernel splits Q and P into: 2 (hi + lo, ~fp32
 // products) or 1 (f16 only)
@@ -96,8 +98,8 @@ __device__ __forceinline__ const _Float16* v_elem(const _Float16* base, int k, i
                                              ((d & 7) << 1));
 }
 
-template <int HD, int RT, int NW, bool RING, int D>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecodeOcc<HD, RT>, 8))) void decode_kernel(DecodeParams p) {
+template <int HD, int RT, int NW, int H, bool RING, int D>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecodeOcc<HD, RT, NW>, 8))) void decode_kernel(DecodeParams p) {
     constexpr int DS = HD / 32;   // 32-dim k-steps of the QK^T MFMA
     constexpr int DT = HD / 16;   // 16-dim output tiles
     constexpr int VPL = HD / 8;   // 16-byte V pieces per lane per block
@@ -109,7 +111,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     __shared__ __attribute__((aligned(16))) char smem[SMEM];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
-    const int kvh = blockIdx.y % p.n_kv, rg = blockIdx.y / p.n_kv;
+    constexpr int W = NW / H;                   // waves per head
+    const int hl = wave % H, wsub = wave / H;   // this wave's head (local) and block phase
+    const int hgroups = p.n_kv / H;
+    const int kvh = (blockIdx.y % hgroups) * H + hl, rg = blockIdx.y / hgroups;
     const int s = blockIdx.z;
     const int len = p.seq_len ? p.seq_len[s] : p.kv_len;
     if (len < p.T || len <= 0) return;
@@ -142,13 +147,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     constexpr int KPL = 64 / PPR;       // keys per 64 lanes
     const int vk0 = lane / PPR;
     const uint32_t vcol = 16 * ((lane % PPR) ^ ((vk0 & 3) << 1));
-    // this wave's blocks: kb = kfirst + 64 * (wave + NW * i)
+    // this wave's blocks: kb = kfirst + 64 * (wsub + W * i)
     int kfirst = kbeg;
     if (lo_min > kbeg) kfirst = kbeg + ((lo_min - kbeg) & ~63);
     const int nblk_all = (kend - kfirst + 63) / 64;
-    const int nb = nblk_all > wave ? (nblk_all - wave + NW - 1) / NW : 0;
+    const int nb = nblk_all > wsub ? (nblk_all - wsub + W - 1) / W : 0;
     char* vlds = smem + wave * VBUF;
-    auto blk = [&](int i) { return kfirst + 64 * (wave + NW * i); };
+    auto blk = [&](int i) { return kfirst + 64 * (wsub + W * i); };
 
     // D blocks in flight: K straight into MFMA-operand registers, V into
     // staging registers
@@ -329,7 +334,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
         }
     }
 
-    // ---- merge the NW wave states of each row through LDS ----
+    // ---- merge the W wave states of each (head, row) through LDS ----
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) l[rt] = group4_sum(l[rt]);
     __syncthreads();  // V buffers are free
@@ -349,26 +354,30 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     __syncthreads();
 
     const int rows_here = min(ROWS, p.R - rbase);
-    // (row, 4-dim chunk) items of the workgroup's result
+    // (head, row, 4-dim chunk) items of the workgroup's result; wave
+    // wsub * H + h holds phase wsub of head h
     constexpr int D4 = HD / 4;
-    for (int it = tid; it < rows_here * D4; it += 64 * NW) {
-        const int row = it / D4, d = 4 * (it % D4);
+    for (int it = tid; it < H * rows_here * D4; it += 64 * NW) {
+        const int h_l = it / (rows_here * D4), rest = it % (rows_here * D4);
+        const int row = rest / D4, d = 4 * (rest % D4);
+        const int kvh_o = (blockIdx.y % hgroups) * H + h_l;
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) M = fmaxf(M, mml[(w * ROWS + row) * 2]);
+        for (int w = 0; w < W; ++w) M = fmaxf(M, mml[((w * H + h_l) * ROWS + row) * 2]);
         const float ms = (M == -INFINITY) ? 0.f : M;
         float L = 0.f;
         float4v O = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int w = 0; w < NW; ++w) {
-            const float wt = fast_exp2(mml[(w * ROWS + row) * 2] - ms);
-            L += mml[(w * ROWS + row) * 2 + 1] * wt;
-            O += *reinterpret_cast<const float4v*>(mo + (w * ROWS + row) * HD + d) * wt;
+        for (int w = 0; w < W; ++w) {
+            const int src = (w * H + h_l) * ROWS + row;
+            const float wt = fast_exp2(mml[src * 2] - ms);
+            L += mml[src * 2 + 1] * wt;
+            O += *reinterpret_cast<const float4v*>(mo + src * HD + d) * wt;
         }
         const int r = rbase + row;
         if (n_active == 1) {
             // the only split: normalise here, sink in max and denominator
-            const int t = r / p.hpk, h = kvh * p.hpk + r % p.hpk;
+            const int t = r / p.hpk, h = kvh_o * p.hpk + r % p.hpk;
             float f;
             if (p.sinks) {
                 const float sk = p.sinks[h] * kLog2e;
@@ -380,7 +389,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
             }
             *reinterpret_cast<float4v*>(p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + d) = O * f;
         } else {
-            const size_t idx = ((size_t)(s * p.n_kv + kvh) * p.R + r) * p.n_slot + slot;
+            const size_t idx = ((size_t)(s * p.n_kv + kvh_o) * p.R + r) * p.n_slot + slot;
             if (d == 0) *reinterpret_cast<float2*>(p.ws_ml + 2 * idx) = make_float2(M, L);
             *reinterpret_cast<float4v*>(p.ws_o + idx * HD + d) = O;
         }
@@ -482,14 +491,14 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
     }
 }
 
-template <int HD, int RT, int NW>
+template <int HD, int RT, int NW, int H>
 static hipError_t launch_k(const DecodeParams& p, hipStream_t st) {
-    dim3 grid(p.n_slot, p.n_kv * p.n_rg, p.n_seq);
+    dim3 grid(p.n_slot, p.n_kv / p.wg_heads * p.n_rg, p.n_seq);
     constexpr int D = kDecodeDepth<HD, RT>;
     {
     ProfScope ps(kProfDecodeSplit, st);
-    if (p.ring_cap) hipLaunchKernelGGL((decode_kernel<HD, RT, NW, true, D>), grid, dim3(64 * NW), 0, st, p);
-    else hipLaunchKernelGGL((decode_kernel<HD, RT, NW, false, D>), grid, dim3(64 * NW), 0, st, p);
+    if (p.ring_cap) hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, true, D>), grid, dim3(64 * NW), 0, st, p);
+    else hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, false, D>), grid, dim3(64 * NW), 0, st, p);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.n_slot == 1) return e;
@@ -498,14 +507,19 @@ static hipError_t launch_k(const DecodeParams& p, hipStream_t st) {
     return hipGetLastError();
 }
 
-hipError_t launch_decode(const DecodeParams& p, int rt, hipStream_t st) {
+hipError_t launch_decode(const DecodeParams& p, int rt, int nw, hipStream_t st) {
     if (p.hd == 64) {
-        if (rt == 1) return launch_k<64, 1, kDecodeWaves>(p, st);
-        if (rt == 2) return launch_k<64, 2, kDecodeWaves>(p, st);
-        if (rt == 4) return launch_k<64, 4, kDecodeWaves>(p, st);
-    } else if (p.hd == 128) {
-        if (rt == 1) return launch_k<128, 1, kDecodeWaves>(p, st);
-        if (rt == 2) return launch_k<128, 2, kDecodeWaves>(p, st);
+        if (nw == 8 && p.wg_heads == 4) {
+            if (rt == 1) return launch_k<64, 1, 8, 4>(p, st);
+            if (rt == 2) return launch_k<64, 2, 8, 4>(p, st);
+        } else if (nw == 4 && p.wg_heads == 1) {
+            if (rt == 1) return launch_k<64, 1, 4, 1>(p, st);
+            if (rt == 2) return launch_k<64, 2, 4, 1>(p, st);
+            if (rt == 4) return launch_k<64, 4, 4, 1>(p, st);
+        }
+    } else if (p.hd == 128 && nw == 4 && p.wg_heads == 1) {
+        if (rt == 1) return launch_k<128, 1, 4, 1>(p, st);
+        if (rt == 2) return launch_k<128, 2, 4, 1>(p, st);
     }
     return hipErrorInvalidValue;
 }

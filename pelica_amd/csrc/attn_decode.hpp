@@ -7,8 +7,10 @@ namespace pelica {
 // most key splits one query row may have (the combine stages one weight per
 // split in LDS)
 constexpr int kMaxSlots = 1024;
-// waves per decode workgroup
-constexpr int kDecodeWaves = 4;
+// Waves per decode workgroup (wg_heads kv heads x the rest waves each): 4,
+// or 8 where two waves per SIMD fit the kernel's registers (head dim 64, up
+// to 32 rows) and the call is large enough to want whole-row reads.
+constexpr bool decode_can_use_8_waves(int hd, int rt) { return hd == 64 && rt <= 2; }
 
 struct DecodeParams {
     const float* q;
@@ -26,9 +28,10 @@ struct DecodeParams {
     float qscale;        // scale * log2(e)
     int n_slot;          // key splits per (sequence, kv head, row group) in the grid
     int split_keys;      // keys per split, a multiple of 64
+    int wg_heads;        // kv heads per workgroup: 4 (8-wave workgroups) or 1
 };
 
-hipError_t launch_decode(const DecodeParams& p, int rt, hipStream_t st);
+hipError_t launch_decode(const DecodeParams& p, int rt, int nw, hipStream_t st);
 // zero n counters with a fill kernel (graph-capturable)
 hipError_t launch_zero(unsigned* p, size_t n, hipStream_t st);
 

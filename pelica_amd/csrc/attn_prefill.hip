@@ -65,16 +65,15 @@ __device__ __forceinline__ int v_slot(int k, int p) {
     return k * (HD * 2) + ((p ^ ((k & 3) << 1)) << 4);
 }
 
-template <int HD, int RT, int NW, bool RING>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(
+template <int HD, int RT, bool RING>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(
     PrefillParams p, int n_tb, int TB) {
+    constexpr int NW = 4;
     constexpr int KS = HD / 16;                 // 16-dim k-steps of QK^T
     constexpr int DT = HD / 32;                 // 32-dim output tiles
-    constexpr int TILE = 64 * HD * 2;           // bytes of a K (or V) tile
+    constexpr int TILE = 64 * HD * 2;           // bytes of a 64-key K (or V) tile
     constexpr int PPR = HD / 8;                 // 16-byte pieces per key row
-    constexpr int PPT = 64 * PPR / (64 * NW);   // pieces per thread (K, and V)
-    static_assert((64 * PPR) % (64 * NW) == 0, "tile pieces must split evenly");
-    __shared__ __attribute__((aligned(16))) char lds[4 * TILE];  // K0 V0 K1 V1
+    __shared__ __attribute__((aligned(16))) char lds[4 * TILE];  // K0 K1 V0 V1
 
     // XCD-aware block order: dispatch goes round-robin over the 8 XCDs, so
     // give each XCD a contiguous range of logical blocks (same kv head)
@@ -106,31 +105,30 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
         (void*)(p.v + row0 * p.row_stride + (size_t)kvh * HD), (short)0, (int)nrec, kBufferFlags);
     const int kb0 = lo_first & ~63;
     const int n_tiles = (pos_last - kb0) / 64 + 1;
-    // thread piece i*64*NW + tid of a tile -> (key, 16-byte column)
-    constexpr int KPI = 64 * NW / PPR;  // keys per piece round
-    const int pkey = tid / PPR, pcol = tid % PPR;
-    u32x4 kr[PPT], vr[PPT];
-    auto load_tile = [&](int kb) {
+    const int n_chunks = 2 * n_tiles;  // 32-key chunks
+    // Tiles go from HBM straight into LDS (buffer_load ... lds): wave
+    // instruction i of wave w fills LDS slots 64 (NW i + w) + lane (16 bytes
+    // each) of a tile; the lane loads the logical piece that the swizzled
+    // layout puts in its slot.
+    constexpr int WI = PPR / NW;  // wave instructions per tile and wave
+    static_assert(PPR % NW == 0, "tile pieces must split evenly over the waves");
+    char* const kbuf = lds;              // K tiles: kbuf + (tile & 1) * TILE
+    char* const vbuf = lds + 2 * TILE;   // V tiles: vbuf + (tile & 1) * TILE
+    auto load_tile = [&](const __amdgpu_buffer_rsrc_t& rs, char* dst, int tile, bool is_v) {
+        const int kb = kb0 + 64 * tile;
 #pragma unroll
-        for (int i = 0; i < PPT; ++i) {
-            const int key = KPI * i + pkey;
-            const uint32_t off = RING ? ((kb + key) % p.ring_cap) * stride_b + 16 * pcol
-                                      : (uint32_t)(kb + key) * stride_b + 16 * pcol;
-            kr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
-            vr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
+        for (int i = 0; i < WI; ++i) {
+            const int slot = 64 * (NW * i + wave) + lane;
+            const int key = slot / PPR, phys = slot % PPR;
+            const int piece = is_v ? phys ^ ((key & 3) << 1) : phys ^ (key & 7);
+            const uint32_t off = RING ? ((kb + key) % p.ring_cap) * stride_b + 16 * piece
+                                      : (uint32_t)(kb + key) * stride_b + 16 * piece;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rs, (__attribute__((address_space(3))) void*)(dst + 1024 * (NW * i + wave)), 16, off, 0, 0, 0);
         }
     };
-    auto store_tile = [&](int buf) {
-        char* kt = lds + buf * 2 * TILE;
-        char* vt = kt + TILE;
-#pragma unroll
-        for (int i = 0; i < PPT; ++i) {
-            const int key = KPI * i + pkey;
-            *reinterpret_cast<u32x4*>(kt + k_slot<HD>(key, pcol)) = kr[i];
-            *reinterpret_cast<u32x4*>(vt + v_slot<HD>(key, pcol)) = vr[i];
-        }
-    };
-    load_tile(kb0);
+    // s_waitcnt vmcnt(0): the tile loads above have landed in LDS
+    auto wait_tiles = [] { __builtin_amdgcn_s_waitcnt(0x0F70); };
 
     // this lane's query rows (column c32 of each 32-row tile): Q as the B
     // operand, position and window start
@@ -158,7 +156,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     float16v o[DT][RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-        m[rt] = -INFINITY;
+        m[rt] = valid[rt] ? -INFINITY : 0.f;  // rows past the block: all masked, fast path
         l[rt] = 0.f;
         if (p.sinks && valid[rt]) {
             const int r = (wave * RT + rt) * 32 + c32;
@@ -169,120 +167,225 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
         for (int dt = 0; dt < DT; ++dt) o[dt][rt] = float16v{};
     }
 
-    store_tile(0);
-    __syncthreads();
-
-    for (int it = 0; it < n_tiles; ++it) {
-        const int kb = kb0 + 64 * it;
-        const int buf = it & 1;
-        const bool more = it + 1 < n_tiles;
-        if (more) load_tile(kb + 64);
-        const char* kt_lds = lds + buf * 2 * TILE;
-        const char* vt_lds = kt_lds + TILE;
-
-        // S^T = K Q^T: 2 key tiles x RT row tiles, k-steps outermost
-        float16v sc[2][RT];
+    // S^T of chunk c (32 keys x RT row tiles): element i of a lane is key
+    // 32 c + 8 (i / 4) + 4 h2 + i % 4 of row c32
+    auto qk = [&](int c, float16v (&sc)[RT]) {
+        const char* kt = kbuf + ((c >> 1) & 1) * TILE;
+        const int krow = 32 * (c & 1) + c32;
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt) sc[kt][rt] = float16v{};
+        for (int rt = 0; rt < RT; ++rt) sc[rt] = float16v{};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-            half8 ka[2];
+            const half8 ka = *reinterpret_cast<const half8*>(kt + k_slot<HD>(krow, 2 * ks + h2));
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-                ka[kt] = *reinterpret_cast<const half8*>(kt_lds + k_slot<HD>(32 * kt + c32, 2 * ks + h2));
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int rt = 0; rt < RT; ++rt) sc[kt][rt] = mfma32(ka[kt], qb[rt][ks], sc[kt][rt]);
+            for (int rt = 0; rt < RT; ++rt) sc[rt] = mfma32(ka, qb[rt][ks], sc[rt]);
         }
-
-        // boundary tiles only: causal / window mask.  Element i of key tile
-        // kt is key kb + 32 kt + 8 (i / 4) + 4 h2 + i % 4.
-        if (kb + 63 > pos_first || kb < lo_last) {
+    };
+    // O^T += V^T P^T over chunk c; pb[w] holds keys 16 w .. 16 w + 15 of it
+    auto pv = [&](int c, const half8 (&pb)[2][RT]) {
+        const char* vt = vbuf + ((c >> 1) & 1) * TILE;
+        const int G = lane >> 4, r4 = (lane & 15) >> 2, q4 = lane & 3;
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int key = kb + 32 * kt + 8 * (i / 4) + 4 * h2 + (i % 4);
-#pragma unroll
-                    for (int rt = 0; rt < RT; ++rt)
-                        if (key < lor[rt] || key > posr[rt]) sc[kt][rt][i] = -INFINITY;
-                }
-        }
-
-        // tile max per row (raw scores; the scale is positive)
-        float bm[RT];
-        bool grow = false;
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-            float x = -INFINITY;
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) x = fmaxf(x, sc[kt][rt][i]);
-            bm[rt] = half_max(x) * p.qscale;
-            grow |= bm[rt] > m[rt] + 8.f;
-        }
-        if (__builtin_amdgcn_ballot_w64(grow)) {
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt) {
-                const float mn = fmaxf(m[rt], bm[rt]);
-                if (mn != m[rt]) {
-                    const float c = fast_exp2(m[rt] - mn);  // 0 when m was -inf
-                    l[rt] *= c;
-#pragma unroll
-                    for (int dt = 0; dt < DT; ++dt) o[dt][rt] *= c;
-                    m[rt] = mn;
-                }
-            }
-        }
-
-        // P = 2^(s*scale - m) as f16 B operands; chunk u (16 keys) is
-        // elements 8(u%2) .. +7 of key tile u/2
-        // (the row sum takes the f16 P the PV product uses, two at a time)
-        half8 pb[4][RT];
-        const half2 one2 = {(_Float16)1.f, (_Float16)1.f};
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-            const float ms = (m[rt] == -INFINITY) ? 0.f : m[rt];
-            float ls = 0.f;
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    pb[u][rt][j] = (_Float16)fast_exp2(__builtin_fmaf(sc[u >> 1][rt][8 * (u & 1) + j], p.qscale, -ms));
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    ls = __builtin_amdgcn_fdot2(half2{pb[u][rt][2 * j], pb[u][rt][2 * j + 1]}, one2, ls, false);
-            }
-            l[rt] += ls;
-        }
-
-        // O^T += V^T P^T
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int w = 0; w < 2; ++w) {
             half8 va[DT];
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
-                // lanes of 16-lane group G read keys 16u + 4 h2 + r (+8) at
+                // lanes of 16-lane group G read keys 16w + 4 h2 + r (+8) at
                 // dims 32 dt + 16 (G & 1) + 4 q; lane 4r + q of the group
-                const int G = lane >> 4, r4 = (lane & 15) >> 2, q4 = lane & 3;
-                const int key = 16 * u + 4 * h2 + r4, dim = 32 * dt + 16 * (G & 1) + 4 * q4;
-                const _Float16* a0 = reinterpret_cast<const _Float16*>(vt_lds + v_slot<HD>(key, dim >> 3) + ((dim & 7) << 1));
-                const _Float16* a1 = reinterpret_cast<const _Float16*>(vt_lds + v_slot<HD>(key + 8, dim >> 3) + ((dim & 7) << 1));
+                const int key = 32 * (c & 1) + 16 * w + 4 * h2 + r4, dim = 32 * dt + 16 * (G & 1) + 4 * q4;
+                const _Float16* a0 = reinterpret_cast<const _Float16*>(vt + v_slot<HD>(key, dim >> 3) + ((dim & 7) << 1));
+                const _Float16* a1 = reinterpret_cast<const _Float16*>(vt + v_slot<HD>(key + 8, dim >> 3) + ((dim & 7) << 1));
                 va[dt] = cat8(lds_read_tr(a0), lds_read_tr(a1));
             }
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-                for (int rt = 0; rt < RT; ++rt) o[dt][rt] = mfma32(va[dt], pb[u][rt], o[dt][rt]);
+                for (int rt = 0; rt < RT; ++rt) o[dt][rt] = mfma32(va[dt], pb[w][rt], o[dt][rt]);
+        }
+    };
+
+    // Software pipeline over 32-key chunks: while the softmax of chunk c
+    // runs on the vector ALUs, the matrix cores take QK^T of chunk c+1 and
+    // PV of chunk c-1.  K tiles and V tiles are double-buffered separately;
+    // one barrier per chunk orders the tile loads against their readers.
+    //
+    // Softmax without a per-chunk max: P = 2^(s*scale - m) with the running
+    // m; a lane whose chunk sum stays <= 2^14 had no overflow or loss (every
+    // P is <= its sum, f16 keeps 11 bits at any magnitude).  Otherwise
+    // (first chunk, a new maximum far above m, masked-out rows) the wave
+    // takes the exact path: chunk max, rescale O and l, recompute P.
+    constexpr float kSumLimit = 16384.f;
+    {
+        // V tile 1's buffer feeds the (empty) PV of chunk -1: zero it
+#pragma unroll
+        for (int i = 0; i < TILE / (16 * 64 * NW); ++i)
+            *reinterpret_cast<u32x4*>(vbuf + TILE + 16 * (tid + 64 * NW * i)) = u32x4{0, 0, 0, 0};
+        load_tile(rk, kbuf, 0, false);
+        if (n_tiles > 1) load_tile(rk, kbuf + TILE, 1, false);
+        load_tile(rv, vbuf, 0, true);
+        wait_tiles();
+    }
+    __syncthreads();
+
+    float16v s_a[RT], s_b[RT];
+    half8 p_a[2][RT], p_b[2][RT];
+#pragma unroll
+    for (int w = 0; w < 2; ++w)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) p_b[w][rt] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+    qk(0, s_a);
+    const half2 one2 = {(_Float16)1.f, (_Float16)1.f};
+
+    // one chunk: scores of c in s_cur, of c+1 into s_nxt; P of c-1 in
+    // p_prv, of c into p_cur
+    auto step = [&](int c, float16v (&s_cur)[RT], float16v (&s_nxt)[RT], const half8 (&p_prv)[2][RT],
+                    half8 (&p_cur)[2][RT]) {
+        // K of tile t+2 and V of tile t+1 at odd chunks c = 2t+1: their
+        // buffers' last readers finished at chunk 2t; first readers at 2t+3
+        const int t = c >> 1;
+        if (c & 1) {
+            if (t + 2 < n_tiles) load_tile(rk, kbuf + (t & 1) * TILE, t + 2, false);
+            if (t + 1 < n_tiles) load_tile(rv, vbuf + ((t + 1) & 1) * TILE, t + 1, true);
         }
 
-        if (more) store_tile(buf ^ 1);
+        const int kb = kb0 + 32 * c;
+        if (kb + 31 > pos_first || kb < lo_last) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int key = kb + 8 * (i / 4) + 4 * h2 + (i % 4);
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt)
+                    if (key < lor[rt] || key > posr[rt]) s_cur[rt][i] = -INFINITY;
+            }
+        }
+
+        // operands: KS K pieces of QK^T (chunk c+1, past the last chunk:
+        // discarded), then 2 DT V pieces of PV (chunk c-1); each read two
+        // operands ahead of its first MFMA
+        constexpr int NOPD = KS + 2 * DT;
+        half8 opd[NOPD];
+        const char* const kt_c = kbuf + (((c + 1) >> 1) & 1) * TILE;
+        const int krow = 32 * ((c + 1) & 1) + c32;
+        const char* const vt_c = vbuf + (((c - 1) >> 1) & 1) * TILE;
+        auto read_opd = [&](int r) {
+            if (r < KS) {
+                opd[r] = *reinterpret_cast<const half8*>(kt_c + k_slot<HD>(krow, 2 * r + h2));
+            } else {
+                // lanes of 16-lane group G read keys 16w + 4 h2 + r4 (+8) at
+                // dims 32 dt + 16 (G & 1) + 4 q4; lane 4 r4 + q4 of the group
+                const int w = (r - KS) / DT, dt = (r - KS) % DT;
+                const int G = lane >> 4, r4 = (lane & 15) >> 2, q4 = lane & 3;
+                const int key = 32 * ((c - 1) & 1) + 16 * w + 4 * h2 + r4, dim = 32 * dt + 16 * (G & 1) + 4 * q4;
+                const _Float16* a0 = reinterpret_cast<const _Float16*>(vt_c + v_slot<HD>(key, dim >> 3) + ((dim & 7) << 1));
+                const _Float16* a1 = reinterpret_cast<const _Float16*>(vt_c + v_slot<HD>(key + 8, dim >> 3) + ((dim & 7) << 1));
+                opd[r] = cat8(lds_read_tr(a0), lds_read_tr(a1));
+            }
+        };
+        read_opd(0);
+        read_opd(1);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) s_nxt[rt] = float16v{};
+
+        // The wave's MFMAs (QK^T of c+1, then PV of c-1) interleaved in
+        // program order with the softmax of chunk c, so the matrix cores and
+        // the vector ALUs work side by side.  The softmax runs as four
+        // stages over all NS scores of the lane (fma, exp2, f16 pack, row-sum
+        // dot), each op far from the one it depends on.
+        constexpr int NM = KS * RT + 2 * DT * RT;  // MFMAs
+        constexpr int NS = 16 * RT;                // scores per lane
+        constexpr int NP = NS / 2;                 // score pairs
+        constexpr int SKEW = 3;                    // pairs between an exp2 and its pack
+        constexpr int NOPS = NS + NP + SKEW + NP;  // fma, (exp2 pair | pack) slots, dot
+        // y = s*scale - ms in place (ms: the running max, 0 while it is -inf,
+        // so the exact path below can recover s*scale = y + ms)
+        float ms[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) ms[rt] = m[rt] == -INFINITY ? 0.f : m[rt];
+        float acc[RT][2];
+        float tmp[2 * (SKEW + 1)];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) acc[rt][0] = acc[rt][1] = 0.f;
+        auto softmax_op = [&](int op) {
+            if (op < NS) {
+                const int rt = op / 16, i = op % 16;
+                s_cur[rt][i] = __builtin_fmaf(s_cur[rt][i], p.qscale, -ms[rt]);
+            } else if (op < NS + NP + SKEW) {
+                const int k = op - NS;  // exp2 of pair k, pack of pair k - SKEW
+                if (k < NP) {
+                    const int rt = k / 8, i = 2 * (k % 8);
+                    tmp[(2 * k) % (2 * (SKEW + 1))] = fast_exp2(s_cur[rt][i]);
+                    tmp[(2 * k + 1) % (2 * (SKEW + 1))] = fast_exp2(s_cur[rt][i + 1]);
+                }
+                if (k >= SKEW) {
+                    const int kk = k - SKEW, rt = kk / 8, i = 2 * (kk % 8);
+                    p_cur[i / 8][rt][i % 8] = (_Float16)tmp[(2 * kk) % (2 * (SKEW + 1))];
+                    p_cur[i / 8][rt][i % 8 + 1] = (_Float16)tmp[(2 * kk + 1) % (2 * (SKEW + 1))];
+                }
+            } else {
+                const int k = op - NS - NP - SKEW, rt = k / 8, i = 2 * (k % 8);
+                acc[rt][k & 1] = __builtin_amdgcn_fdot2(half2{p_cur[i / 8][rt][i % 8], p_cur[i / 8][rt][i % 8 + 1]},
+                                                        one2, acc[rt][k & 1], false);
+            }
+        };
+#pragma unroll
+        for (int i = 0; i < NM; ++i) {
+            const int r = i / RT;  // operand of MFMA i
+            if (i % RT == 0 && r + 2 < NOPD) read_opd(r + 2);
+            if (i < KS * RT) {
+                const int rt = i % RT;
+                s_nxt[rt] = mfma32(opd[r], qb[rt][r], s_nxt[rt]);
+            } else {
+                const int j = i - KS * RT, w = j / (DT * RT), dt = (j / RT) % DT, rt = j % RT;
+                o[dt][rt] = mfma32(opd[r], p_prv[w][rt], o[dt][rt]);
+            }
+#pragma unroll
+            for (int op = i * NOPS / NM; op < (i + 1) * NOPS / NM; ++op) softmax_op(op);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        float ls[RT];
+        bool bad = false;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            ls[rt] = acc[rt][0] + acc[rt][1];
+            bad |= !(ls[rt] <= kSumLimit);
+        }
+        if (__builtin_amdgcn_ballot_w64(bad)) {
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                // s*scale = y + ms
+                float x = -INFINITY;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) x = fmaxf(x, s_cur[rt][i]);
+                const float mn = fmaxf(m[rt], half_max(x) + ms[rt]);
+                if (mn > m[rt]) {
+                    const float cf = fast_exp2(m[rt] - mn);  // 0 when m was -inf
+                    l[rt] *= cf;
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt) o[dt][rt] *= cf;
+                    m[rt] = mn;
+                }
+                const float shift = ms[rt] - (m[rt] == -INFINITY ? 0.f : m[rt]);
+                float a = 0.f;
+#pragma unroll
+                for (int w = 0; w < 2; ++w)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        p_cur[w][rt][j] = (_Float16)fast_exp2(s_cur[rt][8 * w + j] + shift);
+                        a += (float)p_cur[w][rt][j];
+                    }
+                ls[rt] = a;
+            }
+        }
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) l[rt] += ls[rt];
+        if ((c & 1) == 0) wait_tiles();
         __syncthreads();
+    };
+    for (int c = 0; c < n_chunks; c += 2) {  // n_chunks is even
+        step(c, s_a, s_b, p_b, p_a);
+        step(c + 1, s_b, s_a, p_a, p_b);
     }
+    pv(n_chunks - 1, p_b);
 
     // O^T lane layout: dim 32 dt + 8 (i / 4) + 4 h2 + i % 4 of row c32
 #pragma unroll
@@ -304,8 +407,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     }
 }
 
-template <int HD, int RT, int NW>
+template <int HD, int RT>
 static hipError_t launch(const PrefillParams& p, hipStream_t st) {
+    constexpr int NW = 4;
     constexpr int ROWS = NW * RT * 32;
     if (p.hpk > ROWS) return hipErrorNotSupported;
     const int TB = ROWS / p.hpk;
@@ -314,15 +418,15 @@ static hipError_t launch(const PrefillParams& p, hipStream_t st) {
     if (nblk > 0x7fffffff) return hipErrorNotSupported;
     ProfScope ps(kProfPrefill, st);
     if (p.ring_cap)
-        hipLaunchKernelGGL((prefill_kernel<HD, RT, NW, true>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p, n_tb, TB);
+        hipLaunchKernelGGL((prefill_kernel<HD, RT, true>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p, n_tb, TB);
     else
-        hipLaunchKernelGGL((prefill_kernel<HD, RT, NW, false>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p, n_tb, TB);
+        hipLaunchKernelGGL((prefill_kernel<HD, RT, false>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p, n_tb, TB);
     return hipGetLastError();
 }
 
 hipError_t launch_prefill(const PrefillParams& p, hipStream_t st) {
-    if (p.hd == 64) return launch<64, 2, 4>(p, st);
-    if (p.hd == 128) return launch<128, 1, 4>(p, st);
+    if (p.hd == 64) return launch<64, 2>(p, st);
+    if (p.hd == 128) return launch<128, 1>(p, st);
     return hipErrorNotSupported;
 }
 
