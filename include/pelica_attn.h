@@ -96,6 +96,21 @@ int pelica_attn_decode(const PelicaAttnDesc* desc, const float* q, const uint16_
                        const uint16_t* v, const float* sinks, float* out,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/* Decode partials: the same pass as pelica_attn_decode, but instead of the
+ * output it writes the (max, sum, unnormalised O) of the keys this cache
+ * holds, one slot per (sequence, token, head) in merge_dec's format:
+ *   parts[((s*q_tokens + t)*n_head + h)*(hd+2)] = {M, L, O[0..hd)},
+ * M the natural-log max of the scaled scores (-3e38 when no key is
+ * visible), L = sum e^(s-M), O = sum e^(s-M) v.  No sinks: they join in the
+ * final pelica_attn_partials_merge together with the CPU tier's slots.
+ * Workspace as for pelica_attn_decode.  Replaces dec_res, attn_dec over the
+ * VRAM rows into the partial slots `part` (src/moe.rs:1600-1606,
+ * src/moe_kernels.rs:482-583), that src/moe.rs:1713-1729 completes with
+ * the rows past VRAM. */
+int pelica_attn_decode_partials(const PelicaAttnDesc* desc, const float* q, const uint16_t* k,
+                                const uint16_t* v, float* parts, void* workspace,
+                                size_t workspace_bytes, void* stream);
+
 /* Prefill (prompt) attention: f16 queries, f16 cache, f16 output, f32
  * accumulation and softmax, causal with optional window and sinks.
  * Replaces: attn_p (src/oss_prefill.rs:391-526, src/oss.rs:734-741) and

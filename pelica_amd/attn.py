@@ -5,8 +5,8 @@ dispatches (src/moe.rs:1343,1364 decode; src/oss.rs:675-694 gpt-oss decode and
 drafts; src/oss.rs:734-741 prompt) and its CPU tier calls
 ``cpu_attn::chunk(&Shape, kv, k, v, q, out)`` (src/cpu_attn.rs:72).  This
 module mirrors that surface: ``Shape`` is ``cpu_attn::Shape``
-(src/cpu_attn.rs:13-26), ``decode`` / ``prefill`` / ``partials_merge`` are the
-three C entry points.  Errors come back as ``AttnError`` carrying the C status
+(src/cpu_attn.rs:13-26), ``decode`` / ``decode_partials`` / ``prefill`` /
+``partials_merge`` are the C entry points.  Errors come back as ``AttnError`` carrying the C status
 and the library's message (the reference returns ``anyhow::Result`` from its
 engine calls).
 
@@ -35,6 +35,7 @@ EXPORTS = (
     "pelica_attn_workspace_bytes",
     "pelica_attn_workspace_init",
     "pelica_attn_decode",
+    "pelica_attn_decode_partials",
     "pelica_attn_prefill",
     "pelica_attn_partials_merge",
     "pelica_attn_prof_enable",
@@ -127,6 +128,8 @@ def load_library() -> ctypes.CDLL:
     lib.pelica_attn_workspace_init.argtypes = [vp, sz, vp]
     lib.pelica_attn_decode.restype = ctypes.c_int
     lib.pelica_attn_decode.argtypes = [dp, vp, vp, vp, vp, vp, vp, sz, vp]
+    lib.pelica_attn_decode_partials.restype = ctypes.c_int
+    lib.pelica_attn_decode_partials.argtypes = [dp, vp, vp, vp, vp, vp, sz, vp]
     lib.pelica_attn_prefill.restype = ctypes.c_int
     lib.pelica_attn_prefill.argtypes = [dp, vp, vp, vp, vp, vp, vp]
     lib.pelica_attn_partials_merge.restype = ctypes.c_int
@@ -227,6 +230,37 @@ def decode(q, k, v, *, n_kv: int, kv_len: int, sinks=None, window: int = 0, ring
     _check(lib.pelica_attn_decode(ctypes.byref(desc), _ptr(q), _ptr(k), _ptr(v), _ptr(sinks), _ptr(out),
                                   _ptr(workspace), ws_bytes, _stream_ptr(stream)))
     return out
+
+
+def decode_partials(q, k, v, *, n_kv: int, kv_len: int, window: int = 0, ring_cap: int = 0,
+                    scale: Optional[float] = None, seq_kv_len=None, seq_kv_offset=None, kv_row_stride: int = 0,
+                    parts=None, workspace=None, stream=None):
+    """Partials of the keys this cache holds: f32 [n_seq, q_tokens, n_head,
+    hd + 2] slots {M (natural log), L, O} in merge_dec's format, no sinks
+    (they join in ``partials_merge`` with the CPU tier's slots)."""
+    import torch
+
+    assert q.dtype == torch.float32 and q.dim() == 4 and q.is_contiguous() and q.is_cuda
+    assert k.dtype == torch.float16 and v.dtype == torch.float16 and k.is_contiguous() and v.is_contiguous()
+    _validate_lens(seq_kv_len, seq_kv_offset)
+    n_seq, T, n_head, hd = q.shape
+    desc = make_desc(n_head, n_kv, hd, n_seq=n_seq, q_tokens=T, kv_len=kv_len, seq_kv_len=seq_kv_len,
+                     seq_kv_offset=seq_kv_offset, kv_row_stride=kv_row_stride, window=window,
+                     ring_cap=ring_cap, scale=scale)
+    lib = load_library()
+    need = lib.pelica_attn_workspace_bytes(ctypes.byref(desc))
+    if need == 0:
+        msg = lib.pelica_attn_last_error().decode(errors="replace")
+        if msg:
+            raise AttnError(EINVAL, msg)
+    if parts is None:
+        parts = torch.empty(n_seq, T, n_head, hd + 2, dtype=torch.float32, device=q.device)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _check(lib.pelica_attn_decode_partials(ctypes.byref(desc), _ptr(q), _ptr(k), _ptr(v), _ptr(parts),
+                                           _ptr(workspace), ws_bytes, _stream_ptr(stream)))
+    return parts
 
 
 def prefill(q, k, v, *, n_kv: int, kv_len: Optional[int] = None, sinks=None, window: int = 0,

@@ -179,15 +179,23 @@ int pelica_attn_workspace_init(void* workspace, size_t workspace_bytes, void* st
     return PELICA_ATTN_OK;
 }
 
-int pelica_attn_decode(const PelicaAttnDesc* desc, const float* q, const uint16_t* k, const uint16_t* v,
-                       const float* sinks, float* out, void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// decode into out (final, with sinks) or into merge_dec partial slots
+int run_decode(const PelicaAttnDesc* desc, const float* q, const uint16_t* k, const uint16_t* v,
+               const float* sinks, float* out, float* parts, void* workspace, size_t workspace_bytes,
+               void* stream) {
     g_err[0] = 0;
     DecodePlan pl;
     int rc = plan_decode(desc, &pl);
     if (rc) return rc;
-    if (!q || !k || !v || !out) return fail(PELICA_ATTN_EINVAL, "q, k, v and out must be non-NULL");
+    if (!q || !k || !v || !(out || parts))
+        return fail(PELICA_ATTN_EINVAL, "q, k, v and %s must be non-NULL", parts ? "parts" : "out");
     if (misaligned(q) || misaligned(k) || misaligned(v) || misaligned(out) || misaligned(workspace))
         return fail(PELICA_ATTN_EINVAL, "q, k, v, out and workspace must be 16-byte aligned");
+    if (reinterpret_cast<uintptr_t>(parts) % 8) return fail(PELICA_ATTN_EINVAL, "parts must be 8-byte aligned");
     if (pl.ws_bytes && (!workspace || workspace_bytes < pl.ws_bytes))
         return fail(PELICA_ATTN_EWORKSPACE, "workspace of %zu bytes needed, %zu given", pl.ws_bytes,
                     workspace ? workspace_bytes : (size_t)0);
@@ -218,9 +226,29 @@ int pelica_attn_decode(const PelicaAttnDesc* desc, const float* q, const uint16_
     p.n_slot = pl.n_slot;
     p.split_keys = pl.split_keys;
     p.wg_heads = pl.wg_heads;
+    p.parts = parts;
     hipError_t e = pelica::launch_decode(p, pl.rt, pl.nw, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(PELICA_ATTN_EHIP, "decode launch: %s", hipGetErrorString(e));
     return PELICA_ATTN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pelica_attn_decode(const PelicaAttnDesc* desc, const float* q, const uint16_t* k, const uint16_t* v,
+                       const float* sinks, float* out, void* workspace, size_t workspace_bytes, void* stream) {
+    return run_decode(desc, q, k, v, sinks, out, nullptr, workspace, workspace_bytes, stream);
+}
+
+int pelica_attn_decode_partials(const PelicaAttnDesc* desc, const float* q, const uint16_t* k,
+                                const uint16_t* v, float* parts, void* workspace, size_t workspace_bytes,
+                                void* stream) {
+    if (!parts) {
+        g_err[0] = 0;
+        return fail(PELICA_ATTN_EINVAL, "parts must be non-NULL");
+    }
+    return run_decode(desc, q, k, v, nullptr, nullptr, parts, workspace, workspace_bytes, stream);
 }
 
 int pelica_attn_prefill(const PelicaAttnDesc* desc, const uint16_t* q, const uint16_t* k, const uint16_t* v,

@@ -98,6 +98,14 @@ __device__ __forceinline__ const _Float16* v_elem(const _Float16* base, int k, i
                                              ((d & 7) << 1));
 }
 
+// One merge_dec partial slot {M (natural log), L, O[hd]} (8-byte aligned):
+// this thread's 4 dims at d, and the (max, sum) pair from the d == 0 thread.
+__device__ __forceinline__ void store_part(float* slot, int d, float m2, float l, const float4v& o) {
+    if (d == 0) *reinterpret_cast<float2*>(slot) = make_float2(m2 == -INFINITY ? -3.0e38f : m2 * kLn2, l);
+    *reinterpret_cast<float2*>(slot + 2 + d) = make_float2(o[0], o[1]);
+    *reinterpret_cast<float2*>(slot + 4 + d) = make_float2(o[2], o[3]);
+}
+
 template <int HD, int RT, int NW, int H, bool RING, int D>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecodeOcc<HD, RT, NW>, 8))) void decode_kernel(DecodeParams p) {
     constexpr int DS = HD / 32;   // 32-dim k-steps of the QK^T MFMA
@@ -375,7 +383,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
             O += *reinterpret_cast<const float4v*>(mo + src * HD + d) * wt;
         }
         const int r = rbase + row;
-        if (n_active == 1) {
+        if (n_active == 1 && p.parts) {
+            const int t = r / p.hpk, h = kvh_o * p.hpk + r % p.hpk;
+            store_part(p.parts + ((size_t)(s * p.T + t) * p.n_head + h) * (HD + 2), d, M, L, O);
+        } else if (n_active == 1) {
             // the only split: normalise here, sink in max and denominator
             const int t = r / p.hpk, h = kvh_o * p.hpk + r % p.hpk;
             float f;
@@ -438,7 +449,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
         const int c = c0 + tid + 256 * j;
         ml[j] = c <= c1 ? *reinterpret_cast<const float2*>(p.ws_ml + 2 * (base + c)) : make_float2(-INFINITY, 0.f);
     }
-    const float sk = p.sinks ? p.sinks[h] * kLog2e : -INFINITY;
+    const float sk = (p.sinks && !p.parts) ? p.sinks[h] * kLog2e : -INFINITY;
     float M = sk;
 #pragma unroll
     for (int j = 0; j < MLJ; ++j) M = fmaxf(M, ml[j].x);
@@ -460,7 +471,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
     if (lane == 0) s_red[wave] = L;
     __syncthreads();
     L = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
-    if (p.sinks) L += fast_exp2(sk - ms);
+    if (p.sinks && !p.parts) L += fast_exp2(sk - ms);
 
     float4v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -487,7 +498,10 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
         float4v sum = s_o[tid];
 #pragma unroll
         for (int q = 1; q < PH; ++q) sum += s_o[q * D4 + tid];
-        *reinterpret_cast<float4v*>(p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + d) = sum * (1.f / L);
+        if (p.parts)
+            store_part(p.parts + ((size_t)(s * p.T + t) * p.n_head + h) * (HD + 2), d, M, L, sum);
+        else
+            *reinterpret_cast<float4v*>(p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + d) = sum * (1.f / L);
     }
 }
 

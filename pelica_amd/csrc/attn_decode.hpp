@@ -29,6 +29,7 @@ struct DecodeParams {
     int n_slot;          // key splits per (sequence, kv head, row group) in the grid
     int split_keys;      // keys per split, a multiple of 64
     int wg_heads;        // kv heads per workgroup: 4 (8-wave workgroups) or 1
+    float* parts;        // non-null: write merge_dec partial slots here instead of out
 };
 
 hipError_t launch_decode(const DecodeParams& p, int rt, int nw, hipStream_t st);
