@@ -128,6 +128,39 @@ int pelica_attn_partials_merge(int32_t n_head, int32_t hd, int32_t n_parts,
                                const float* parts, const float* sinks, float* out,
                                void* stream);
 
+/* ---- the step before attention ----------------------------------------- */
+
+/* Rotary embedding table: (cos, sin) float pairs, rot/2 pairs per row.
+ * table_split == 0: row = position (the gpt-oss table, src/oss.rs:1320-1349,
+ * read at src/oss_batch.rs:151-152).  table_split = n > 0: the two-level
+ * table of src/moe.rs:484-519 — rows < n hold positions 256 i, rows n + p
+ * the positions p < 256 — composed by angle addition
+ * (src/moe_kernels.rs:350-355). */
+typedef struct PelicaRope {
+    int32_t rot;          /* rotated dims at the start of each head: even, <= hd; 0 = no rope */
+    int32_t neox;         /* 1: pairs (j, j + rot/2) (NeoX, gpt-oss); 0: pairs (2j, 2j + 1) */
+    int32_t table_split;  /* 0, or the number of 256-position rows (see above) */
+    int32_t table_rows;   /* rows in table (positions are checked against it) */
+    const float* table;   /* device [table_rows][rot/2][2] */
+} PelicaRope;
+
+/* What follows the q, k, v projections of the pass's tokens, in one launch:
+ * per-head RMS norm of q and k heads (x * inv * w, inv = 1/sqrt(mean x^2 +
+ * eps)) when q_norm / k_norm are given, rope on q and k, q written back in
+ * place, the k and v rows rounded to f16 into the cache.  Token t of
+ * sequence s sits at position len_s - q_tokens + t and its row is
+ * seq_kv_offset[s] + (ring_cap ? pos % ring_cap : pos) (as for attention).
+ * q: [n_seq*q_tokens tokens][n_head][hd], k, v: [tokens][n_kv][hd] f32; token
+ * i's heads start at i * token_stride floats (0: dense per tensor; the
+ * engine's fused [q | k | v] rows use (n_head + 2 n_kv) hd).  hd: 64, 128
+ * or 256.  Replaces qk_dec (src/moe_kernels.rs:304-378, src/moe.rs:1322-1340)
+ * and ROPE_KV_T (src/oss_batch.rs:113-170), writing f16 rows where gpt-oss
+ * kept f32 ones (src/oss.rs:615-616). */
+int pelica_attn_qkv_rope_cache(const PelicaAttnDesc* desc, const PelicaRope* rope, float* q,
+                               const float* k, const float* v, int64_t token_stride,
+                               const float* q_norm, const float* k_norm, float eps,
+                               uint16_t* k_cache, uint16_t* v_cache, void* stream);
+
 /* ---- per-kernel GPU timing ------------------------------------------- */
 
 /* kernel ids of PelicaAttnProfRecord */
@@ -135,6 +168,7 @@ int pelica_attn_partials_merge(int32_t n_head, int32_t hd, int32_t n_parts,
 #define PELICA_ATTN_PROF_DECODE_COMBINE 2
 #define PELICA_ATTN_PROF_PREFILL 3
 #define PELICA_ATTN_PROF_MERGE 4
+#define PELICA_ATTN_PROF_QKV 5
 
 typedef struct PelicaAttnProfRecord {
     int32_t kernel; /* PELICA_ATTN_PROF_* */

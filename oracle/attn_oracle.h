@@ -86,6 +86,33 @@ int orc_attn_f16(const OrcDesc* d, const uint16_t* q, const uint16_t* k, const u
 int orc_partials(const OrcDesc* d, const float* q, const uint16_t* k, const uint16_t* v,
                  int s, int t, int k_begin, int k_end, float* parts, int threads);
 
+/* ---- the step before attention (oracle/qkv_oracle.c) ------------------ */
+
+/* Rotary table: (cos, sin) pairs, rot/2 pairs per row.  table_split == 0:
+ * row = position (ROPE_KV_T's table, src/oss_batch.rs:151-152, built by
+ * src/oss.rs:1320-1349).  table_split = n > 0: rows < n hold positions 256 i,
+ * rows n + p the positions p < 256, and a position's angle is composed from
+ * rows pos/256 and n + pos%256 by angle addition (qk_dec,
+ * src/moe_kernels.rs:350-355; table src/moe.rs:484-519). */
+typedef struct OrcRope {
+    int32_t rot;          /* rotated dims: the first rot of each head (even, <= hd) */
+    int32_t neox;         /* 1: pairs (j, j + rot/2); 0: pairs (2j, 2j + 1) */
+    int32_t table_split;  /* see above */
+    const float* table;
+} OrcRope;
+
+/* What follows the q, k, v projections, per token (token t of sequence s at
+ * position len_s - q_tokens + t): per-head RMS norm of q and k heads when
+ * q_norm / k_norm are given (x * inv * w, inv = 1/sqrt(sum x^2 / hd + eps)),
+ * rope on q and k, q written back, k and v rounded to f16 (nearest even)
+ * into cache row seq_kv_off[s] + (ring_cap ? pos % ring_cap : pos).
+ * q: [n_seq][q_tokens][n_head][hd], k, v: [n_seq][q_tokens][n_kv][hd] f32.
+ * qk_dec (src/moe_kernels.rs:304-378), ROPE_KV_T (src/oss_batch.rs:113-170).
+ * Returns 0, or -1 on a bad descriptor. */
+int orc_qk_norm_rope_cache(const OrcDesc* d, const OrcRope* r, float* q, const float* k, const float* v,
+                           const float* q_norm, const float* k_norm, float eps,
+                           uint16_t* k_cache, uint16_t* v_cache);
+
 #ifdef __cplusplus
 }
 #endif

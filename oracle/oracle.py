@@ -25,6 +25,15 @@ def build() -> str:
     return LIB_PATH
 
 
+class OrcRope(ctypes.Structure):
+    _fields_ = [
+        ("rot", ctypes.c_int32),
+        ("neox", ctypes.c_int32),
+        ("table_split", ctypes.c_int32),
+        ("table", ctypes.c_void_p),
+    ]
+
+
 class OrcDesc(ctypes.Structure):
     _fields_ = [
         ("n_head", ctypes.c_int32),
@@ -69,6 +78,8 @@ def lib() -> ctypes.CDLL:
         L.orc_attn_f16.argtypes = [dp, vp, vp, vp, vp, vp, i32, i32, i32]
         L.orc_partials.restype = i32
         L.orc_partials.argtypes = [dp, vp, vp, vp, i32, i32, i32, i32, vp, i32]
+        L.orc_qk_norm_rope_cache.restype = i32
+        L.orc_qk_norm_rope_cache.argtypes = [dp, ctypes.POINTER(OrcRope), vp, vp, vp, vp, vp, ctypes.c_float, vp, vp]
         _lib = L
     return _lib
 
@@ -181,3 +192,58 @@ def partials(q, k, v, *, n_kv, kv_len, s=0, t=0, k_begin=0, k_end=None, sinks=No
     if n < 0:
         raise ValueError("oracle rejected the descriptor")
     return out[:n]
+
+
+def rope_table(n_pos, rot, base=10000.0, split=False):
+    """(cos, sin) table [rows, rot/2, 2] f32 for plain rotary angles
+    theta = pos * base^(-2j/rot), computed in f64 like the engines' tables
+    (src/oss.rs:1320-1349, src/moe.rs:484-519, without YaRN).  split=True
+    gives the two-level layout: rows pos = 256 i (i < n_hi), then pos = p
+    (p < 256); returns (table, n_hi)."""
+    half = rot // 2
+    freq = base ** (-(2.0 * np.arange(half)) / rot)
+    if split:
+        n_hi = -(-n_pos // 256)
+        pos = np.concatenate([256.0 * np.arange(n_hi), np.arange(256.0)])
+    else:
+        n_hi = 0
+        pos = np.arange(float(n_pos))
+    th = pos[:, None] * freq[None, :]
+    t = np.stack([np.cos(th), np.sin(th)], -1).astype(np.float32)
+    return (t, n_hi) if split else t
+
+
+def qk_norm_rope_cache(q, k, v, *, n_kv, kv_len=None, seq_kv_len=None, seq_kv_offset=None, ring_cap=0,
+                       kv_row_stride=0, cache_rows=None, k_cache=None, v_cache=None, rot=None, neox=True,
+                       table=None, table_split=0, q_norm=None, k_norm=None, eps=1e-6):
+    """Oracle of the step before attention.  q f32 [n_seq, T, n_head, hd]
+    (returned rotated), k, v f32 [n_seq, T, n_kv, hd]; the new rows land in
+    uint16 (f16 bits) caches, returned (given ones are updated)."""
+    n_seq, T, n_head, hd = q.shape
+    q = np.array(q, np.float32, copy=True)
+    k = _c(k, np.float32)
+    v = _c(v, np.float32)
+    if seq_kv_len is None:
+        seq_kv_len = np.full(n_seq, kv_len, np.int32)
+    seq_kv_len = _c(seq_kv_len, np.int32)
+    if seq_kv_offset is None:
+        span = ring_cap or int(seq_kv_len.max())
+        seq_kv_offset = np.arange(n_seq, dtype=np.int64) * span
+    seq_kv_offset = _c(seq_kv_offset, np.int64)
+    stride = kv_row_stride or n_kv * hd
+    if k_cache is None:
+        rows = cache_rows or int(seq_kv_offset.max()) + (ring_cap or int(seq_kv_len.max()))
+        k_cache = np.zeros((rows, stride), np.uint16)
+        v_cache = np.zeros((rows, stride), np.uint16)
+    d = _desc(n_head, n_kv, hd, n_seq, T, seq_kv_len, seq_kv_offset, stride, 0, ring_cap, None)
+    r = None
+    if table is not None:
+        table = _c(table, np.float32)
+        r = OrcRope(rot or hd, 1 if neox else 0, table_split, _p(table))
+    qn = _c(q_norm, np.float32)
+    kn = _c(k_norm, np.float32)
+    rc = lib().orc_qk_norm_rope_cache(ctypes.byref(d), None if r is None else ctypes.byref(r), _p(q), _p(k), _p(v),
+                                      _p(qn), _p(kn), eps, _p(k_cache), _p(v_cache))
+    if rc != 0:
+        raise ValueError("oracle rejected the descriptor")
+    return q, k_cache, v_cache

@@ -38,12 +38,13 @@ EXPORTS = (
     "pelica_attn_decode_partials",
     "pelica_attn_prefill",
     "pelica_attn_partials_merge",
+    "pelica_attn_qkv_rope_cache",
     "pelica_attn_prof_enable",
     "pelica_attn_prof_read",
 )
 
 #: kernel ids of the per-kernel timing records
-PROF_KERNELS = {1: "decode_split", 2: "decode_combine", 3: "prefill", 4: "partials_merge"}
+PROF_KERNELS = {1: "decode_split", 2: "decode_combine", 3: "prefill", 4: "partials_merge", 5: "qkv_rope_cache"}
 
 
 class AttnError(RuntimeError):
@@ -70,6 +71,18 @@ class Shape:
     @property
     def n_head(self) -> int:
         return self.n_kv * self.hpk
+
+
+class Rope(ctypes.Structure):
+    """``PelicaRope``: rotary dims, NeoX pairing, table layout and rows."""
+
+    _fields_ = [
+        ("rot", ctypes.c_int32),
+        ("neox", ctypes.c_int32),
+        ("table_split", ctypes.c_int32),
+        ("table_rows", ctypes.c_int32),
+        ("table", ctypes.c_void_p),
+    ]
 
 
 class ProfRecord(ctypes.Structure):
@@ -132,6 +145,9 @@ def load_library() -> ctypes.CDLL:
     lib.pelica_attn_decode_partials.argtypes = [dp, vp, vp, vp, vp, vp, sz, vp]
     lib.pelica_attn_prefill.restype = ctypes.c_int
     lib.pelica_attn_prefill.argtypes = [dp, vp, vp, vp, vp, vp, vp]
+    lib.pelica_attn_qkv_rope_cache.restype = ctypes.c_int
+    lib.pelica_attn_qkv_rope_cache.argtypes = [dp, ctypes.POINTER(Rope), vp, vp, vp, ctypes.c_int64, vp, vp,
+                                               ctypes.c_float, vp, vp, vp]
     lib.pelica_attn_partials_merge.restype = ctypes.c_int
     lib.pelica_attn_partials_merge.argtypes = [i32, i32, i32, vp, vp, vp, vp]
     lib.pelica_attn_prof_enable.restype = ctypes.c_int
@@ -261,6 +277,38 @@ def decode_partials(q, k, v, *, n_kv: int, kv_len: int, window: int = 0, ring_ca
     _check(lib.pelica_attn_decode_partials(ctypes.byref(desc), _ptr(q), _ptr(k), _ptr(v), _ptr(parts),
                                            _ptr(workspace), ws_bytes, _stream_ptr(stream)))
     return parts
+
+
+def qkv_rope_cache(q, k, v, k_cache, v_cache, *, n_kv: int, kv_len: int, table=None, rot: int = 0,
+                   neox: bool = True, table_split: int = 0, q_norm=None, k_norm=None, eps: float = 1e-6,
+                   seq_kv_len=None, seq_kv_offset=None, ring_cap: int = 0, kv_row_stride: int = 0,
+                   token_stride: int = 0, n_seq: Optional[int] = None, q_tokens: Optional[int] = None,
+                   n_head: Optional[int] = None, hd: Optional[int] = None, stream=None):
+    """The step before attention (qk_dec / ROPE_KV_T): per-head RMS norm of
+    q and k (when q_norm / k_norm are given), rope on q and k (table: f32
+    [rows, rot/2, 2] cos/sin), q rotated in place, k and v rows into the f16
+    caches.  q: f32 [n_seq, T, n_head, hd], k, v: f32 [n_seq, T, n_kv, hd]
+    (or views into one fused buffer with ``token_stride``; then pass the
+    shape keywords).  Returns q."""
+    import torch
+
+    if n_seq is None:
+        n_seq, q_tokens, n_head, hd = q.shape
+    assert q.dtype == k.dtype == v.dtype == torch.float32 and q.is_cuda
+    assert k_cache.dtype == v_cache.dtype == torch.float16
+    _validate_lens(seq_kv_len, seq_kv_offset)
+    desc = make_desc(n_head, n_kv, hd, n_seq=n_seq, q_tokens=q_tokens, kv_len=kv_len, seq_kv_len=seq_kv_len,
+                     seq_kv_offset=seq_kv_offset, kv_row_stride=kv_row_stride, ring_cap=ring_cap)
+    rp = None
+    if table is not None:
+        assert table.dtype == torch.float32 and table.is_cuda and table.is_contiguous()
+        rot = rot or hd
+        rp = Rope(rot, 1 if neox else 0, table_split, table.shape[0], table.data_ptr())
+    lib = load_library()
+    _check(lib.pelica_attn_qkv_rope_cache(ctypes.byref(desc), None if rp is None else ctypes.byref(rp), _ptr(q),
+                                          _ptr(k), _ptr(v), token_stride, _ptr(q_norm), _ptr(k_norm), eps,
+                                          _ptr(k_cache), _ptr(v_cache), _stream_ptr(stream)))
+    return q
 
 
 def prefill(q, k, v, *, n_kv: int, kv_len: Optional[int] = None, sinks=None, window: int = 0,

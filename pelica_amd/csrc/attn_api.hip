@@ -9,6 +9,7 @@
 #include "../../include/pelica_attn.h"
 #include "attn_decode.hpp"
 #include "attn_prefill.hpp"
+#include "attn_qkv.hpp"
 #include "attn_prof.hpp"
 
 namespace {
@@ -249,6 +250,69 @@ int pelica_attn_decode_partials(const PelicaAttnDesc* desc, const float* q, cons
         return fail(PELICA_ATTN_EINVAL, "parts must be non-NULL");
     }
     return run_decode(desc, q, k, v, nullptr, nullptr, parts, workspace, workspace_bytes, stream);
+}
+
+int pelica_attn_qkv_rope_cache(const PelicaAttnDesc* desc, const PelicaRope* rope, float* q, const float* k,
+                               const float* v, int64_t token_stride, const float* q_norm, const float* k_norm,
+                               float eps, uint16_t* k_cache, uint16_t* v_cache, void* stream) {
+    g_err[0] = 0;
+    if (!desc) return fail(PELICA_ATTN_EINVAL, "desc is NULL");
+    const PelicaAttnDesc* d = desc;
+    if (d->hd != 64 && d->hd != 128 && d->hd != 256) return fail(PELICA_ATTN_EUNSUPPORTED, "hd %d (64, 128 or 256)", d->hd);
+    if (d->n_head <= 0 || d->n_kv <= 0 || d->n_head % d->n_kv) return fail(PELICA_ATTN_EINVAL, "bad head counts");
+    if (d->n_seq <= 0 || d->q_tokens <= 0 || d->q_tokens > 65535 || d->n_seq > 65535)
+        return fail(PELICA_ATTN_EINVAL, "n_seq and q_tokens must be in [1, 65535]");
+    if (d->kv_len < d->q_tokens) return fail(PELICA_ATTN_EINVAL, "kv_len %d < q_tokens %d", d->kv_len, d->q_tokens);
+    if ((d->seq_kv_len == nullptr) != (d->seq_kv_offset == nullptr) && d->seq_kv_len)
+        return fail(PELICA_ATTN_EINVAL, "seq_kv_len needs seq_kv_offset");
+    if (d->ring_cap < 0 || (d->ring_cap && d->ring_cap < d->q_tokens))
+        return fail(PELICA_ATTN_EINVAL, "ring_cap %d cannot hold the pass's %d rows", d->ring_cap, d->q_tokens);
+    if (d->flags) return fail(PELICA_ATTN_EINVAL, "flags must be 0");
+    if (!q || !k || !v || !k_cache || !v_cache) return fail(PELICA_ATTN_EINVAL, "q, k, v and the caches must be non-NULL");
+    const int64_t stride = d->kv_row_stride ? d->kv_row_stride : (int64_t)d->n_kv * d->hd;
+    if (stride < (int64_t)d->n_kv * d->hd) return fail(PELICA_ATTN_EINVAL, "kv_row_stride below n_kv * hd");
+    const int64_t tq = token_stride ? token_stride : (int64_t)d->n_head * d->hd;
+    const int64_t tkv = token_stride ? token_stride : (int64_t)d->n_kv * d->hd;
+    if (token_stride && token_stride < (int64_t)d->n_kv * d->hd)
+        return fail(PELICA_ATTN_EINVAL, "token_stride below a token's heads");
+    if (!(eps >= 0.f)) return fail(PELICA_ATTN_EINVAL, "eps must be >= 0");
+    pelica::QkvParams p{};
+    if (rope && rope->rot) {
+        if (rope->rot < 0 || rope->rot % 2 || rope->rot > d->hd) return fail(PELICA_ATTN_EINVAL, "rot %d", rope->rot);
+        if (!rope->table || rope->table_split < 0) return fail(PELICA_ATTN_EINVAL, "rope table missing");
+        if (rope->table_split && rope->table_rows < rope->table_split + 256)
+            return fail(PELICA_ATTN_EINVAL, "a two-level rope table needs %d rows", rope->table_split + 256);
+        const long long covered = rope->table_split ? 256LL * rope->table_split : rope->table_rows;
+        if (covered < d->kv_len)
+            return fail(PELICA_ATTN_EINVAL, "rope table covers %lld positions, kv_len is %d", covered, d->kv_len);
+        p.table = rope->table;
+        p.rot = rope->rot;
+        p.neox = rope->neox ? 1 : 0;
+        p.table_split = rope->table_split;
+    }
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.tok_q = tq;
+    p.tok_kv = tkv;
+    p.q_norm = q_norm;
+    p.k_norm = k_norm;
+    p.eps = eps;
+    p.k_cache = k_cache;
+    p.v_cache = v_cache;
+    p.seq_len = d->seq_kv_len;
+    p.seq_off = d->seq_kv_offset;
+    p.row_stride = stride;
+    p.kv_len = d->kv_len;
+    p.n_head = d->n_head;
+    p.n_kv = d->n_kv;
+    p.hd = d->hd;
+    p.T = d->q_tokens;
+    p.n_seq = d->n_seq;
+    p.ring_cap = d->ring_cap;
+    hipError_t e = pelica::launch_qkv(p, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(PELICA_ATTN_EHIP, "qkv launch: %s", hipGetErrorString(e));
+    return PELICA_ATTN_OK;
 }
 
 int pelica_attn_prefill(const PelicaAttnDesc* desc, const uint16_t* q, const uint16_t* k, const uint16_t* v,

@@ -8,7 +8,7 @@
 
 namespace pelica {
 
-enum ProfKernel { kProfDecodeSplit = 1, kProfDecodeCombine = 2, kProfPrefill = 3, kProfMerge = 4 };
+enum ProfKernel { kProfDecodeSplit = 1, kProfDecodeCombine = 2, kProfPrefill = 3, kProfMerge = 4, kProfQkv = 5 };
 
 bool prof_enabled();
 // opens a record (start event) for `kind` on `st`; returns a handle or -1
