@@ -118,6 +118,23 @@ int pelica_attn_decode_partials(const PelicaAttnDesc* desc, const float* q, cons
 int pelica_attn_prefill(const PelicaAttnDesc* desc, const uint16_t* q, const uint16_t* k,
                         const uint16_t* v, const float* sinks, uint16_t* out, void* stream);
 
+/* Prompt attention over one round of keys: the cache rows of key positions
+ * [key_begin, key_end) (k_rows / v_rows row 0 = position key_begin, e.g. a
+ * staging copy of rows that live past HBM) folded into a running state per
+ * (token, head), state[(t*n_head + h)*(hd+2)] = {M natural-log, L, O[hd]}
+ * (unnormalised), f32.  first = 1 starts the state empty (its contents are
+ * not read).  Rounds must come in key order; after the round that holds key
+ * position len-1 the state is complete.  out (optional, f16
+ * [q_tokens][n_head][hd]) receives the output so far, with the sinks, 0 for
+ * rows that have seen no key.  One sequence, linear cache; causal and window
+ * masks as pelica_attn_prefill.  Replaces attn_pre + attn_fold over
+ * 16K-key rounds of VRAM and staged rows (src/moe_kernels.rs:810-990,
+ * dispatched src/moe.rs:1609-1627). */
+int pelica_attn_prefill_round(const PelicaAttnDesc* desc, const uint16_t* q, const uint16_t* k_rows,
+                              const uint16_t* v_rows, int32_t key_begin, int32_t key_end,
+                              const float* sinks, float* state, int32_t first, uint16_t* out,
+                              void* stream);
+
 /* Combine n_parts partial slots of one decode token (parts[(c*n_head+h)*(hd+2)],
  * natural-log max) in slot order, with optional sinks, into out[n_head][hd].
  * Slots whose max is -3e38 (or -inf) carry no weight, as the reference's

@@ -37,6 +37,7 @@ EXPORTS = (
     "pelica_attn_decode",
     "pelica_attn_decode_partials",
     "pelica_attn_prefill",
+    "pelica_attn_prefill_round",
     "pelica_attn_partials_merge",
     "pelica_attn_qkv_rope_cache",
     "pelica_attn_prof_enable",
@@ -145,6 +146,8 @@ def load_library() -> ctypes.CDLL:
     lib.pelica_attn_decode_partials.argtypes = [dp, vp, vp, vp, vp, vp, sz, vp]
     lib.pelica_attn_prefill.restype = ctypes.c_int
     lib.pelica_attn_prefill.argtypes = [dp, vp, vp, vp, vp, vp, vp]
+    lib.pelica_attn_prefill_round.restype = ctypes.c_int
+    lib.pelica_attn_prefill_round.argtypes = [dp, vp, vp, vp, i32, i32, vp, vp, i32, vp, vp]
     lib.pelica_attn_qkv_rope_cache.restype = ctypes.c_int
     lib.pelica_attn_qkv_rope_cache.argtypes = [dp, ctypes.POINTER(Rope), vp, vp, vp, ctypes.c_int64, vp, vp,
                                                ctypes.c_float, vp, vp, vp]
@@ -332,6 +335,28 @@ def prefill(q, k, v, *, n_kv: int, kv_len: Optional[int] = None, sinks=None, win
     lib = load_library()
     _check(lib.pelica_attn_prefill(ctypes.byref(desc), _ptr(q), _ptr(k), _ptr(v), _ptr(sinks), _ptr(out),
                                    _stream_ptr(stream)))
+    return out
+
+
+def prefill_round(q, k_rows, v_rows, state, *, n_kv: int, kv_len: int, key_begin: int, key_end: int,
+                  first: bool, sinks=None, window: int = 0, scale: Optional[float] = None,
+                  kv_row_stride: int = 0, out=None, stream=None):
+    """Prompt attention over one round of keys [key_begin, key_end) (rows of
+    those positions in k_rows / v_rows), folded into ``state`` (f32 [1, T,
+    n_head, hd + 2]: M natural-log, L, O); ``out`` (f16 like q) gets the
+    output so far when given.  Returns out (or None)."""
+    import torch
+
+    assert q.dtype == torch.float16 and q.dim() == 4 and q.is_contiguous() and q.is_cuda
+    assert k_rows.dtype == v_rows.dtype == torch.float16 and k_rows.is_contiguous() and v_rows.is_contiguous()
+    n_seq, T, n_head, hd = q.shape
+    assert state.dtype == torch.float32 and state.numel() == n_seq * T * n_head * (hd + 2)
+    desc = make_desc(n_head, n_kv, hd, n_seq=n_seq, q_tokens=T, kv_len=kv_len, kv_row_stride=kv_row_stride,
+                     window=window, scale=scale)
+    lib = load_library()
+    _check(lib.pelica_attn_prefill_round(ctypes.byref(desc), _ptr(q), _ptr(k_rows), _ptr(v_rows), key_begin,
+                                         key_end, _ptr(sinks), _ptr(state), 1 if first else 0, _ptr(out),
+                                         _stream_ptr(stream)))
     return out
 
 

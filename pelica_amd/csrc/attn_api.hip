@@ -348,6 +348,46 @@ int pelica_attn_prefill(const PelicaAttnDesc* desc, const uint16_t* q, const uin
     return PELICA_ATTN_OK;
 }
 
+int pelica_attn_prefill_round(const PelicaAttnDesc* desc, const uint16_t* q, const uint16_t* k_rows,
+                              const uint16_t* v_rows, int32_t key_begin, int32_t key_end, const float* sinks,
+                              float* state, int32_t first, uint16_t* out, void* stream) {
+    g_err[0] = 0;
+    int rc = check_desc(desc);
+    if (rc) return rc;
+    if (desc->n_seq != 1 || desc->ring_cap || desc->seq_kv_len)
+        return fail(PELICA_ATTN_EINVAL, "rounds take one sequence of a linear cache");
+    if (!q || !k_rows || !v_rows || !state) return fail(PELICA_ATTN_EINVAL, "q, k_rows, v_rows and state must be non-NULL");
+    if (misaligned(q) || misaligned(k_rows) || misaligned(v_rows) || misaligned(out))
+        return fail(PELICA_ATTN_EINVAL, "q, k_rows, v_rows and out must be 16-byte aligned");
+    if (reinterpret_cast<uintptr_t>(state) % 4) return fail(PELICA_ATTN_EINVAL, "state must be 4-byte aligned");
+    if (key_begin < 0 || key_end <= key_begin || key_end > desc->kv_len)
+        return fail(PELICA_ATTN_EINVAL, "round [%d, %d) outside the %d keys", key_begin, key_end, desc->kv_len);
+    pelica::PrefillParams p{};
+    p.q = q;
+    p.k = k_rows;
+    p.v = v_rows;
+    p.sinks = sinks;
+    p.out = out;
+    p.row_stride = desc->kv_row_stride ? desc->kv_row_stride : (int64_t)desc->n_kv * desc->hd;
+    p.kv_len = desc->kv_len;
+    p.n_head = desc->n_head;
+    p.n_kv = desc->n_kv;
+    p.hd = desc->hd;
+    p.hpk = desc->n_head / desc->n_kv;
+    p.T = desc->q_tokens;
+    p.n_seq = 1;
+    p.window = desc->window;
+    p.qscale = eff_scale(desc) * pelica::kLog2e;
+    p.key_begin = key_begin;
+    p.key_end = key_end;
+    p.first = first ? 1 : 0;
+    p.state = state;
+    hipError_t e = pelica::launch_prefill(p, static_cast<hipStream_t>(stream));
+    if (e == hipErrorNotSupported) return fail(PELICA_ATTN_EUNSUPPORTED, "prefill shape unsupported");
+    if (e != hipSuccess) return fail(PELICA_ATTN_EHIP, "prefill launch: %s", hipGetErrorString(e));
+    return PELICA_ATTN_OK;
+}
+
 int pelica_attn_partials_merge(int32_t n_head, int32_t hd, int32_t n_parts, const float* parts, const float* sinks,
                                float* out, void* stream) {
     g_err[0] = 0;

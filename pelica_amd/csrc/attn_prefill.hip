@@ -65,7 +65,7 @@ __device__ __forceinline__ int v_slot(int k, int p) {
     return k * (HD * 2) + ((p ^ ((k & 3) << 1)) << 4);
 }
 
-template <int HD, int RT, bool RING>
+template <int HD, int RT, bool RING, bool ROUND>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(
     PrefillParams p, int n_tb, int TB) {
     constexpr int NW = 4;
@@ -97,14 +97,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
     // K/V tile loads through buffer resources over this sequence's rows of kv
     // head kvh: 32-bit offsets; rows past the sequence read as 0 (masked)
+    // keys this launch covers: the whole cache, or one round's rows
+    const int kbeg = ROUND ? p.key_begin : 0, kend = ROUND ? min(p.key_end, len) : len;
     const uint32_t stride_b = (uint32_t)p.row_stride * 2;
-    const uint32_t nrec = (RING ? (uint32_t)p.ring_cap : (uint32_t)len) * stride_b;
+    const uint32_t nrec = (RING ? (uint32_t)p.ring_cap : (uint32_t)(kend - kbeg)) * stride_b;
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(p.k + row0 * p.row_stride + (size_t)kvh * HD), (short)0, (int)nrec, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(p.v + row0 * p.row_stride + (size_t)kvh * HD), (short)0, (int)nrec, kBufferFlags);
-    const int kb0 = lo_first & ~63;
-    const int n_tiles = (pos_last - kb0) / 64 + 1;
+    const int kb0 = max(lo_first, kbeg) & ~63;
+    const int klast = min(pos_last, kend - 1);
+    const int n_tiles = klast >= kb0 ? (klast - kb0) / 64 + 1 : 0;  // 0: a round past these tokens
     const int n_chunks = 2 * n_tiles;  // 32-key chunks
     // Tiles go from HBM straight into LDS (buffer_load ... lds): wave
     // instruction i of wave w fills LDS slots 64 (NW i + w) + lane (16 bytes
@@ -121,8 +124,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const int slot = 64 * (NW * i + wave) + lane;
             const int key = slot / PPR, phys = slot % PPR;
             const int piece = is_v ? phys ^ ((key & 3) << 1) : phys ^ (key & 7);
+            // (round rows before key_begin wrap to offsets past nrec: zeros)
             const uint32_t off = RING ? ((kb + key) % p.ring_cap) * stride_b + 16 * piece
-                                      : (uint32_t)(kb + key) * stride_b + 16 * piece;
+                                      : (uint32_t)(kb + key - kbeg) * stride_b + 16 * piece;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rs, (__attribute__((address_space(3))) void*)(dst + 1024 * (NW * i + wave)), 16, off, 0, 0, 0);
         }
@@ -158,13 +162,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int rt = 0; rt < RT; ++rt) {
         m[rt] = valid[rt] ? -INFINITY : 0.f;  // rows past the block: all masked, fast path
         l[rt] = 0.f;
-        if (p.sinks && valid[rt]) {
+        if (!ROUND && p.sinks && valid[rt]) {
             const int r = (wave * RT + rt) * 32 + c32;
             m[rt] = p.sinks[kvh * p.hpk + r % p.hpk] * kLog2e;
             l[rt] = h2 == 0 ? 1.f : 0.f;
         }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) o[dt][rt] = float16v{};
+        if (ROUND && !p.first && valid[rt]) {
+            // the running state of the rounds before (sum split over h2 lanes)
+            const int r = (wave * RT + rt) * 32 + c32;
+            const int t = t0 + r / p.hpk, h = kvh * p.hpk + r % p.hpk;
+            const float* st = p.state + ((size_t)(s * p.T + t) * p.n_head + h) * (HD + 2);
+            m[rt] = st[0] <= -1.0e38f ? -INFINITY : st[0] * kLog2e;
+            l[rt] = h2 == 0 ? st[1] : 0.f;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[dt][rt][i] = st[2 + 32 * dt + 8 * (i / 4) + 4 * h2 + i % 4];
+        }
     }
 
     // S^T of chunk c (32 keys x RT row tiles): element i of a lane is key
@@ -211,10 +227,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     //
     // Softmax without a per-chunk max: P = 2^(s*scale - m) with the running
     // m; a lane whose chunk sum stays <= 2^14 had no overflow or loss (every
-    // P is <= its sum, f16 keeps 11 bits at any magnitude).  Otherwise
-    // (first chunk, a new maximum far above m, masked-out rows) the wave
-    // takes the exact path: chunk max, rescale O and l, recompute P.
+    // P is <= its sum, f16 keeps 11 bits at any magnitude), and once m is
+    // some key's score (or the sink) that key's own term keeps l >= 1, so
+    // terms flushed to 0 are negligible.  Otherwise (no max yet, a new
+    // maximum far above m) the wave takes the exact path: chunk max, rescale
+    // O and l, recompute P.
     constexpr float kSumLimit = 16384.f;
+    if (n_tiles > 0) {  // (uniform over the workgroup)
     {
         // V tile 1's buffer feeds the (empty) PV of chunk -1: zero it
 #pragma unroll
@@ -249,13 +268,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
 
         const int kb = kb0 + 32 * c;
-        if (kb + 31 > pos_first || kb < lo_last) {
+        if (kb + 31 > pos_first || kb < lo_last || (ROUND && (kb < kbeg || kb + 31 >= kend))) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int key = kb + 8 * (i / 4) + 4 * h2 + (i % 4);
+                const bool out_of_round = ROUND && (key < kbeg || key >= kend);
 #pragma unroll
                 for (int rt = 0; rt < RT; ++rt)
-                    if (key < lor[rt] || key > posr[rt]) s_cur[rt][i] = -INFINITY;
+                    if (key < lor[rt] || key > posr[rt] || out_of_round) s_cur[rt][i] = -INFINITY;
             }
         }
 
@@ -347,7 +367,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
             ls[rt] = acc[rt][0] + acc[rt][1];
-            bad |= !(ls[rt] <= kSumLimit);
+            bad |= !(ls[rt] <= kSumLimit) || m[rt] == -INFINITY;  // no max yet: the exact path sets it
         }
         if (__builtin_amdgcn_ballot_w64(bad)) {
 #pragma unroll
@@ -386,6 +406,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         step(c + 1, s_b, s_a, p_a, p_b);
     }
     pv(n_chunks - 1, p_b);
+    }
 
     // O^T lane layout: dim 32 dt + 8 (i / 4) + 4 h2 + i % 4 of row c32
 #pragma unroll
@@ -394,7 +415,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         if (!valid[rt]) continue;
         const int r = (wave * RT + rt) * 32 + c32;
         const int t = t0 + r / p.hpk, h = kvh * p.hpk + r % p.hpk;
-        const float inv = 1.f / lt;
+        float inv = 1.f / lt;
+        if (ROUND) {
+            float* st = p.state + ((size_t)(s * p.T + t) * p.n_head + h) * (HD + 2);
+            if (h2 == 0) {
+                st[0] = m[rt] == -INFINITY ? -3.0e38f : m[rt] * kLn2;
+                st[1] = lt;
+            }
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) st[2 + 32 * dt + 8 * (i / 4) + 4 * h2 + i % 4] = o[dt][rt][i];
+            if (!p.out) continue;
+            // the output so far: sink in max and denominator; 0 before any key
+            if (p.sinks) {
+                const float sk = p.sinks[h] * kLog2e;
+                const float M2 = fmaxf(m[rt], sk);
+                const float w = m[rt] == -INFINITY ? 0.f : fast_exp2(m[rt] - M2);
+                inv = w / (lt * w + fast_exp2(sk - M2));
+            } else {
+                inv = lt > 0.f ? inv : 0.f;
+            }
+        }
         uint16_t* op = p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + 4 * h2;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
@@ -417,10 +459,12 @@ static hipError_t launch(const PrefillParams& p, hipStream_t st) {
     const long long nblk = (long long)n_tb * p.n_kv * p.n_seq;
     if (nblk > 0x7fffffff) return hipErrorNotSupported;
     ProfScope ps(kProfPrefill, st);
-    if (p.ring_cap)
-        hipLaunchKernelGGL((prefill_kernel<HD, RT, true>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p, n_tb, TB);
+    if (p.state)
+        hipLaunchKernelGGL((prefill_kernel<HD, RT, false, true>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p, n_tb, TB);
+    else if (p.ring_cap)
+        hipLaunchKernelGGL((prefill_kernel<HD, RT, true, false>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p, n_tb, TB);
     else
-        hipLaunchKernelGGL((prefill_kernel<HD, RT, false>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p, n_tb, TB);
+        hipLaunchKernelGGL((prefill_kernel<HD, RT, false, false>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p, n_tb, TB);
     return hipGetLastError();
 }
 

@@ -16,6 +16,11 @@ struct PrefillParams {
     int kv_len, n_head, n_kv, hd, hpk, T, n_seq;
     int window, ring_cap;
     float qscale;  // scale * log2(e)
+    // round mode (a prompt's keys in rounds): k, v hold the rows of key
+    // positions [key_begin, key_end); state is the running (M natural-log,
+    // L, O[hd]) per (token, head), read unless first; out may be null
+    int key_begin, key_end, first;
+    float* state;
 };
 
 // hipErrorNotSupported for shapes the kernel does not take

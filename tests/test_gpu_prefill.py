@@ -90,3 +90,23 @@ def test_prefill_matches_decode_rows():
     dec = attn.decode(inp.q[:, -1:].float().contiguous(), inp.k, inp.v, n_kv=8, kv_len=500, sinks=inp.sinks)
     torch.cuda.synchronize()
     assert_close(as_f64(pre[:, -1:]), as_f64(dec), atol=2e-3, rtol=1e-3, what="prefill vs decode")
+
+
+@pytest.mark.parametrize("logit", [-40.0, -120.0])
+def test_all_logits_far_below_zero(logit):
+    # every key has the same score, far below 0 (no sinks): the softmax is
+    # uniform, the output the causal mean of V — the kernel must not lose
+    # the keys to f16 underflow before it has a running max
+    T, L, hd = 300, 700, 64
+    cfg = wl.AttnConfig("neg", "prefill", 8, 8, hd, L, q_tokens=T, seed=31)
+    inp = wl.make_inputs(cfg, "cuda")
+    k0 = torch.randn(hd, device="cuda")
+    k0 = k0 / k0.norm() * 4.0
+    inp.k.copy_(k0.half().expand_as(inp.k))
+    kf = inp.k[0, 0].float()
+    qv = kf * (logit * np.sqrt(hd) / float(kf @ kf))
+    inp.q.copy_(qv.half().expand_as(inp.q))
+    print(f"[case] logit {logit}", flush=True)
+    got = gpu_run(inp)
+    ref = oracle_run(inp)
+    assert_close(as_f64(got), as_f64(ref), what=f"logit {logit}")
