@@ -111,6 +111,19 @@ int pelica_attn_decode_partials(const PelicaAttnDesc* desc, const float* q, cons
                                 const uint16_t* v, float* parts, void* workspace,
                                 size_t workspace_bytes, void* stream);
 
+/* MLA (latent) attention: one kv head whose keys and values are the same
+ * latent cache rows, hd = 512 f16 per position (row stride kv_row_stride,
+ * 0 = 512); n_kv must be 1; q: the absorbed f32 queries
+ * [n_seq][q_tokens][n_head][512], out f32 alike; token t sees positions
+ * <= len - q_tokens + t (causal, no window, no sinks); scale as given (the
+ * engine passes 1/sqrt(qk_nope)).  Workspace from
+ * pelica_attn_mla_workspace_bytes.  Replaces mla (src/gpu.rs:262-307,
+ * src/forward.rs:936-960), whose latent cache is f32; the f16 rows here are
+ * the same switch as gpt-oss's. */
+size_t pelica_attn_mla_workspace_bytes(const PelicaAttnDesc* desc);
+int pelica_attn_mla(const PelicaAttnDesc* desc, const float* q, const uint16_t* latent, float* out,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
 /* Prefill (prompt) attention: f16 queries, f16 cache, f16 output, f32
  * accumulation and softmax, causal with optional window and sinks.
  * Replaces: attn_p (src/oss_prefill.rs:391-526, src/oss.rs:734-741) and

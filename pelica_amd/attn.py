@@ -36,6 +36,8 @@ EXPORTS = (
     "pelica_attn_workspace_init",
     "pelica_attn_decode",
     "pelica_attn_decode_partials",
+    "pelica_attn_mla_workspace_bytes",
+    "pelica_attn_mla",
     "pelica_attn_prefill",
     "pelica_attn_prefill_round",
     "pelica_attn_partials_merge",
@@ -146,6 +148,10 @@ def load_library() -> ctypes.CDLL:
     lib.pelica_attn_decode_partials.argtypes = [dp, vp, vp, vp, vp, vp, sz, vp]
     lib.pelica_attn_prefill.restype = ctypes.c_int
     lib.pelica_attn_prefill.argtypes = [dp, vp, vp, vp, vp, vp, vp]
+    lib.pelica_attn_mla_workspace_bytes.restype = sz
+    lib.pelica_attn_mla_workspace_bytes.argtypes = [dp]
+    lib.pelica_attn_mla.restype = ctypes.c_int
+    lib.pelica_attn_mla.argtypes = [dp, vp, vp, vp, vp, sz, vp]
     lib.pelica_attn_prefill_round.restype = ctypes.c_int
     lib.pelica_attn_prefill_round.argtypes = [dp, vp, vp, vp, i32, i32, vp, vp, i32, vp, vp]
     lib.pelica_attn_qkv_rope_cache.restype = ctypes.c_int
@@ -335,6 +341,35 @@ def prefill(q, k, v, *, n_kv: int, kv_len: Optional[int] = None, sinks=None, win
     lib = load_library()
     _check(lib.pelica_attn_prefill(ctypes.byref(desc), _ptr(q), _ptr(k), _ptr(v), _ptr(sinks), _ptr(out),
                                    _stream_ptr(stream)))
+    return out
+
+
+def mla(q, latent, *, kv_len: int, scale: Optional[float] = None, seq_kv_len=None, seq_kv_offset=None,
+        kv_row_stride: int = 0, out=None, workspace=None, stream=None):
+    """MLA latent attention: q f32 [n_seq, T, n_head, 512] (absorbed
+    queries), latent f16 cache rows of 512 (keys = values); causal.
+    Returns f32 like q."""
+    import torch
+
+    assert q.dtype == torch.float32 and q.dim() == 4 and q.is_contiguous() and q.is_cuda and q.shape[-1] == 512
+    assert latent.dtype == torch.float16 and latent.is_contiguous()
+    _validate_lens(seq_kv_len, seq_kv_offset)
+    n_seq, T, n_head, hd = q.shape
+    desc = make_desc(n_head, 1, hd, n_seq=n_seq, q_tokens=T, kv_len=kv_len, seq_kv_len=seq_kv_len,
+                     seq_kv_offset=seq_kv_offset, kv_row_stride=kv_row_stride, scale=scale)
+    lib = load_library()
+    need = lib.pelica_attn_mla_workspace_bytes(ctypes.byref(desc))
+    if need == 0:
+        msg = lib.pelica_attn_last_error().decode(errors="replace")
+        if msg:
+            raise AttnError(EINVAL, msg)
+    if out is None:
+        out = torch.empty_like(q)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _check(lib.pelica_attn_mla(ctypes.byref(desc), _ptr(q), _ptr(latent), _ptr(out), _ptr(workspace), ws_bytes,
+                               _stream_ptr(stream)))
     return out
 
 

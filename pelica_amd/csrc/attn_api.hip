@@ -35,13 +35,18 @@ bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) !=
 int ceil_div(long long a, long long b) { return (int)((a + b - 1) / b); }
 
 // Checks shared by decode and prefill.
-int check_desc(const PelicaAttnDesc* d) {
+// mla: the latent layout (hd 512, one kv head, no window or ring)
+int check_desc(const PelicaAttnDesc* d, bool mla = false) {
     if (!d) return fail(PELICA_ATTN_EINVAL, "desc is NULL");
     if (d->flags != 0) return fail(PELICA_ATTN_EINVAL, "flags must be 0 (got %u)", d->flags);
     if (d->n_head <= 0 || d->n_kv <= 0 || d->n_head % d->n_kv)
         return fail(PELICA_ATTN_EINVAL, "n_head %d must be a positive multiple of n_kv %d", d->n_head, d->n_kv);
-    if (d->hd != 64 && d->hd != 128)
+    if (mla) {
+        if (d->hd != 512 || d->n_kv != 1 || d->window || d->ring_cap)
+            return fail(PELICA_ATTN_EUNSUPPORTED, "MLA takes hd 512, n_kv 1, no window or ring");
+    } else if (d->hd != 64 && d->hd != 128) {
         return fail(PELICA_ATTN_EUNSUPPORTED, "hd %d unsupported (64 or 128)", d->hd);
+    }
     if (d->n_seq <= 0 || d->q_tokens <= 0)
         return fail(PELICA_ATTN_EINVAL, "n_seq %d and q_tokens %d must be positive", d->n_seq, d->q_tokens);
     if (d->kv_len < d->q_tokens)
@@ -126,6 +131,36 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
     pl->ctr_bytes = 0;
     pl->ml_bytes = (n_part * 2 * 4 + 255) & ~(size_t)255;
     pl->ws_bytes = n_slot > 1 ? pl->ctr_bytes + pl->ml_bytes + n_part * d->hd * 4 : 0;
+    return PELICA_ATTN_OK;
+}
+
+// MLA: rows = tokens x heads in row groups of 16 RT; 32-key blocks split so
+// ~one workgroup per CU streams the latent (one workgroup fills a CU's LDS)
+int plan_mla(const PelicaAttnDesc* d, DecodePlan* pl) {
+    int rc = check_desc(d, true);
+    if (rc) return rc;
+    const int R = d->q_tokens * d->n_head;
+    const int rt = R <= 16 ? 1 : R <= 32 ? 2 : 4;
+    const int n_rg = ceil_div(R, 16 * rt);
+    const long long blocks = (long long)ceil_div(d->kv_len, 32) * n_rg * d->n_seq;
+    const int target = std::max(1, env_int("PELICA_ATTN_MLA_WORKGROUPS", 256));
+    long long split_keys = 32LL * std::max<long long>(1, (blocks + target - 1) / target);
+    int n_slot = ceil_div(d->kv_len, split_keys);
+    while (n_slot > pelica::kMaxSlots) {
+        split_keys *= 2;
+        n_slot = ceil_div(d->kv_len, split_keys);
+    }
+    pl->R = R;
+    pl->rt = rt;
+    pl->n_rg = n_rg;
+    pl->split_keys = (int)split_keys;
+    pl->n_slot = n_slot;
+    pl->wg_heads = 1;
+    pl->nw = 4;
+    const size_t n_part = (size_t)d->n_seq * R * n_slot;
+    pl->ctr_bytes = 0;
+    pl->ml_bytes = (n_part * 2 * 4 + 255) & ~(size_t)255;
+    pl->ws_bytes = n_slot > 1 ? pl->ml_bytes + n_part * 512 * 4 : 0;
     return PELICA_ATTN_OK;
 }
 
@@ -345,6 +380,54 @@ int pelica_attn_prefill(const PelicaAttnDesc* desc, const uint16_t* q, const uin
     hipError_t e = pelica::launch_prefill(p, static_cast<hipStream_t>(stream));
     if (e == hipErrorNotSupported) return fail(PELICA_ATTN_EUNSUPPORTED, "prefill shape unsupported");
     if (e != hipSuccess) return fail(PELICA_ATTN_EHIP, "prefill launch: %s", hipGetErrorString(e));
+    return PELICA_ATTN_OK;
+}
+
+size_t pelica_attn_mla_workspace_bytes(const PelicaAttnDesc* desc) {
+    g_err[0] = 0;
+    DecodePlan pl;
+    if (plan_mla(desc, &pl)) return 0;
+    return pl.ws_bytes;
+}
+
+int pelica_attn_mla(const PelicaAttnDesc* desc, const float* q, const uint16_t* latent, float* out, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+    g_err[0] = 0;
+    DecodePlan pl;
+    int rc = plan_mla(desc, &pl);
+    if (rc) return rc;
+    if (!q || !latent || !out) return fail(PELICA_ATTN_EINVAL, "q, latent and out must be non-NULL");
+    if (misaligned(q) || misaligned(latent) || misaligned(out) || misaligned(workspace))
+        return fail(PELICA_ATTN_EINVAL, "q, latent, out and workspace must be 16-byte aligned");
+    if (pl.ws_bytes && (!workspace || workspace_bytes < pl.ws_bytes))
+        return fail(PELICA_ATTN_EWORKSPACE, "workspace of %zu bytes needed, %zu given", pl.ws_bytes,
+                    workspace ? workspace_bytes : (size_t)0);
+    pelica::DecodeParams p{};
+    p.q = q;
+    p.k = latent;
+    p.v = latent;
+    p.out = out;
+    char* ws = static_cast<char*>(workspace);
+    p.ws_ml = pl.ws_bytes ? reinterpret_cast<float*>(ws) : nullptr;
+    p.ws_o = pl.ws_bytes ? reinterpret_cast<float*>(ws + pl.ml_bytes) : nullptr;
+    p.seq_len = desc->seq_kv_len;
+    p.seq_off = desc->seq_kv_offset;
+    p.row_stride = desc->kv_row_stride ? desc->kv_row_stride : 512;
+    p.kv_len = desc->kv_len;
+    p.n_head = desc->n_head;
+    p.n_kv = 1;
+    p.hd = 512;
+    p.hpk = desc->n_head;
+    p.T = desc->q_tokens;
+    p.R = pl.R;
+    p.n_rg = pl.n_rg;
+    p.n_seq = desc->n_seq;
+    p.qscale = eff_scale(desc) * pelica::kLog2e;
+    p.n_slot = pl.n_slot;
+    p.split_keys = pl.split_keys;
+    p.wg_heads = 1;
+    hipError_t e = pelica::launch_mla(p, pl.rt, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(PELICA_ATTN_EHIP, "mla launch: %s", hipGetErrorString(e));
     return PELICA_ATTN_OK;
 }
 

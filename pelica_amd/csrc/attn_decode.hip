@@ -415,7 +415,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
 template <int HD>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
     constexpr int D4 = HD / 4;
-    constexpr int PH = 256 / D4;        // phases: 16 (hd 64) or 8 (hd 128)
+    constexpr int PH = 256 / D4;        // phases: 16 (hd 64), 8 (hd 128), 2 (hd 512)
     constexpr int J = 16;               // splits per thread per pass
     __shared__ float s_w[kMaxSlots];
     __shared__ float s_red[256 / 64];
@@ -516,8 +516,18 @@ static hipError_t launch_k(const DecodeParams& p, hipStream_t st) {
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.n_slot == 1) return e;
+    return launch_combine(p, st);
+}
+
+hipError_t launch_combine(const DecodeParams& p, hipStream_t st) {
     ProfScope ps(kProfDecodeCombine, st);
-    hipLaunchKernelGGL((decode_combine_kernel<HD>), dim3(p.R, p.n_kv, p.n_seq), dim3(256), 0, st, p);
+    const dim3 grid(p.R, p.n_kv, p.n_seq);
+    switch (p.hd) {
+        case 64: hipLaunchKernelGGL(decode_combine_kernel<64>, grid, dim3(256), 0, st, p); break;
+        case 128: hipLaunchKernelGGL(decode_combine_kernel<128>, grid, dim3(256), 0, st, p); break;
+        case 512: hipLaunchKernelGGL(decode_combine_kernel<512>, grid, dim3(256), 0, st, p); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

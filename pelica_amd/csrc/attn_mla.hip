@@ -1,0 +1,249 @@
+// MLA (latent) attention for gfx950: one shared kv "head" whose keys and
+// values are the same latent cache rows (512 f16 per position), f32
+// absorbed queries [seq][token][head][512], f32 output — the mla kernel of
+// src/gpu.rs:262-307 (called from src/forward.rs:936-960), as split-K
+// flash-decode with an in-order combine.
+//
+// Work split.  A workgroup of 4 waves owns (sequence, row group of RT x 16
+// query rows = (token, head) pairs, key split).  Latent blocks of 32 keys
+// (32 KB) go from HBM straight into LDS (buffer_load ... lds, double
+// buffered); K = V, so each block is read from HBM once for both products.
+// Wave w owns dims [128 w, 128 w + 128): it computes the partial scores
+// S_w^T = K[:, dims] Q[:, dims]^T on v_mfma_f32_16x16x32_f16 (Q split into
+// f16 hi + lo parts, ~fp32 products), the four partials are summed through
+// LDS, every wave runs the same online softmax (base 2), and wave w
+// accumulates O^T[dims] += V^T[dims] P^T with V read by the transposing
+// ds_read_b64_tr_b16 (P split into hi + lo as the B operand).  HBM-bound:
+// per 32-key block 32 KB of latent against 128 MFMAs per wave.
+#include "attn_decode.hpp"
+#include "attn_prof.hpp"
+
+namespace pelica {
+
+namespace {
+
+constexpr int kBufFlags = 0x00020000;  // raw buffer, 32-bit format
+constexpr int kMlaHd = 512;
+
+// LDS byte offset of 16-byte piece p of key row k in a latent block: pieces
+// XOR-swizzled by the key's low 4 bits so 16 consecutive keys read at one
+// piece index hit 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int mla_slot(int k, int p) { return k * (kMlaHd * 2) + ((p ^ (k & 15)) << 4); }
+
+__device__ __forceinline__ const _Float16* mla_elem(const char* base, int k, int d) {
+    return reinterpret_cast<const _Float16*>(base + mla_slot(k, d >> 3) + ((d & 7) << 1));
+}
+
+}  // namespace
+
+template <int RT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void mla_kernel(DecodeParams p) {
+    constexpr int HD = kMlaHd, NW = 4, KB = 32;  // dims, waves, keys per block
+    constexpr int DS = HD / NW / 32;             // 32-dim k-steps per wave (4)
+    constexpr int DT = HD / NW / 16;             // 16-dim output tiles per wave (8)
+    constexpr int ROWS = 16 * RT, NP = 2;
+    constexpr int BLK = KB * HD * 2;             // 32 KB
+    __shared__ __attribute__((aligned(16))) char lds[2 * BLK + NW * ROWS * KB * 4];
+    float* const part = reinterpret_cast<float*>(lds + 2 * BLK);  // [NW][ROWS][KB] partial scores
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+    const int rg = blockIdx.y, s = blockIdx.z, slot = blockIdx.x;
+    const int len = p.seq_len ? p.seq_len[s] : p.kv_len;
+    if (len < p.T || len <= 0) return;
+    const int n_active = min(p.n_slot, (len - 1) / p.split_keys + 1);
+    if (slot >= n_active) return;
+    const int64_t row0 = p.seq_off ? p.seq_off[s] : (int64_t)s * p.kv_len;
+    const int kbeg = slot * p.split_keys, kend = min(kbeg + p.split_keys, len);
+    const int nblk = (kend - kbeg + KB - 1) / KB;
+    const int rbase = rg * ROWS;
+
+    const uint32_t stride_b = (uint32_t)p.row_stride * 2;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.k + row0 * p.row_stride), (short)0, (int)((uint32_t)len * stride_b), kBufFlags);
+    // block i -> LDS buffer i & 1; wave instruction j of wave w fills key row
+    // 4 j + w (64 slots of 16 bytes); the lane loads the piece its slot holds
+    auto load_block = [&](int i) {
+        char* dst = lds + (i & 1) * BLK;
+        const int kb = kbeg + KB * i;
+#pragma unroll
+        for (int j = 0; j < KB / NW; ++j) {
+            const int key = NW * j + wave;
+            const int piece = lane ^ (key & 15);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rs, (__attribute__((address_space(3))) void*)(dst + key * (HD * 2)), 16,
+                (uint32_t)(kb + key) * stride_b + 16 * piece, 0, 0, 0);
+        }
+    };
+    load_block(0);
+
+    // queries of this lane's rows, this wave's dims, f16 hi + lo, base 2
+    half8 qf[NP][RT][DS];
+    int posr[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const int r = rbase + 16 * rt + c16;
+        const bool ok = r < p.R;
+        const int rr = ok ? r : 0;
+        const int t = rr / p.hpk, h = rr % p.hpk;
+        const float* qp = p.q + ((size_t)(s * p.T + t) * p.n_head + h) * HD + 128 * wave + 8 * g;
+        posr[rt] = ok ? len - p.T + t : -1;
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+            const float4v a = *reinterpret_cast<const float4v*>(qp + 32 * ds);
+            const float4v b = *reinterpret_cast<const float4v*>(qp + 32 * ds + 4);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float x = ok ? (j < 4 ? a[j] : b[j - 4]) * p.qscale : 0.f;
+                const _Float16 hi = (_Float16)x;
+                qf[0][rt][ds][j] = hi;
+                qf[1][rt][ds][j] = (_Float16)(x - (float)hi);
+            }
+        }
+    }
+
+    float m[RT], l[RT];
+    float4v o[DT][RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        m[rt] = -INFINITY;
+        l[rt] = 0.f;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[dt][rt] = float4v{0.f, 0.f, 0.f, 0.f};
+    }
+
+    for (int i = 0; i < nblk; ++i) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): block i is in LDS
+        __syncthreads();                     // ... for every wave; block i-1's readers are done
+        if (i + 1 < nblk) load_block(i + 1);
+        const char* blk = lds + (i & 1) * BLK;
+        const int kb = kbeg + KB * i;
+
+        // partial scores over this wave's dims: 2 key tiles x RT row tiles
+        float4v acc[NP][2][RT];
+#pragma unroll
+        for (int pp = 0; pp < NP; ++pp)
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) acc[pp][kt][rt] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+            half8 ka[2];
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+                ka[kt] = *reinterpret_cast<const half8*>(blk + mla_slot(16 * kt + c16, 16 * wave + 4 * ds + g));
+#pragma unroll
+            for (int pp = 0; pp < NP; ++pp)
+#pragma unroll
+                for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt) acc[pp][kt][rt] = mfma16(ka[kt], qf[pp][rt][ds], acc[pp][kt][rt]);
+        }
+        // element i of (kt, rt) is key 16 kt + 4 g + i of row 16 rt + c16
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+                *reinterpret_cast<float4v*>(part + (wave * ROWS + 16 * rt + c16) * KB + 16 * kt + 4 * g) =
+                    acc[0][kt][rt] + acc[1][kt][rt];
+        __syncthreads();
+        float4v sc[2][RT];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                float4v t4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int w = 0; w < NW; ++w)
+                    t4 += *reinterpret_cast<const float4v*>(part + (w * ROWS + 16 * rt + c16) * KB + 16 * kt + 4 * g);
+                sc[kt][rt] = t4;
+            }
+
+        // causal mask and online softmax (identical in every wave)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int key = kb + 16 * kt + 4 * g + e;
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt)
+                    if (key >= kend || key > posr[rt]) sc[kt][rt][e] = -INFINITY;
+            }
+        half8 pf[NP][RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            float bm = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) bm = fmaxf(bm, sc[kt][rt][e]);
+            bm = group4_max(bm);
+            const float mn = fmaxf(m[rt], bm);
+            const float ms = (mn == -INFINITY) ? 0.f : mn;
+            const float c = fast_exp2(m[rt] - ms);
+            m[rt] = mn;
+            float ls = 0.f;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float pe = fast_exp2(sc[kt][rt][e] - ms);
+                    ls += pe;
+                    const _Float16 hi = (_Float16)pe;
+                    pf[0][rt][kt * 4 + e] = hi;
+                    pf[1][rt][kt * 4 + e] = (_Float16)(pe - (float)hi);
+                }
+            l[rt] = l[rt] * c + ls;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o[dt][rt] *= c;
+        }
+
+        // O^T[this wave's dims] += V^T P^T (keys in the B operand's order)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const int k0 = 4 * g + (c16 >> 2), d0 = 128 * wave + 16 * dt + 4 * (c16 & 3);
+            const half8 va = cat8(lds_read_tr(mla_elem(blk, k0, d0)), lds_read_tr(mla_elem(blk, k0 + 16, d0)));
+#pragma unroll
+            for (int pp = 0; pp < NP; ++pp)
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) o[dt][rt] = mfma16(va, pf[pp][rt], o[dt][rt]);
+        }
+    }
+
+    // this wave's dims of each row: the output, or the split's partial
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const float L = group4_sum(l[rt]);
+        const int r = rbase + 16 * rt + c16;
+        if (r >= p.R) continue;
+        const int t = r / p.hpk, h = r % p.hpk;
+        if (n_active == 1) {
+            const float inv = 1.f / L;
+            float* op = p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + 128 * wave + 4 * g;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<float4v*>(op + 16 * dt) = o[dt][rt] * inv;
+        } else {
+            const size_t idx = ((size_t)s * p.R + r) * p.n_slot + slot;
+            if (wave == 0 && g == 0) *reinterpret_cast<float2*>(p.ws_ml + 2 * idx) = make_float2(m[rt], L);
+            float* op = p.ws_o + idx * HD + 128 * wave + 4 * g;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<float4v*>(op + 16 * dt) = o[dt][rt];
+        }
+    }
+}
+
+hipError_t launch_mla(const DecodeParams& p, int rt, hipStream_t st) {
+    const dim3 grid(p.n_slot, p.n_rg, p.n_seq);
+    {
+        ProfScope ps(kProfDecodeSplit, st);
+        if (rt == 1) hipLaunchKernelGGL(mla_kernel<1>, grid, dim3(256), 0, st, p);
+        else if (rt == 2) hipLaunchKernelGGL(mla_kernel<2>, grid, dim3(256), 0, st, p);
+        else if (rt == 4) hipLaunchKernelGGL(mla_kernel<4>, grid, dim3(256), 0, st, p);
+        else return hipErrorInvalidValue;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || p.n_slot == 1) return e;
+    return launch_combine(p, st);
+}
+
+}  // namespace pelica
