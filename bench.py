@@ -167,6 +167,59 @@ def bench_prefill(cfg, steps, warmup):
                 kernel_TFLOPs=flops / (kms * 1e-3) / 1e12)
 
 
+def bench_mla(steps, warmup, n_head=32, kv_len=32768):
+    """MLA decode over a 32K latent cache (not a BASELINE config; reported
+    beside them): bytes = latent rows once + q + out."""
+    import torch
+
+    from pelica_amd import attn
+
+    g = torch.Generator(device="cuda").manual_seed(12)
+    q = torch.randn(1, 1, n_head, 512, generator=g, device="cuda") * 0.25
+    lat = (torch.randn(kv_len, 512, generator=g, device="cuda") * 0.5).half()
+    lats = rotating_copies(lat)
+    out = torch.empty_like(q)
+    desc = attn.make_desc(n_head, 1, 512, kv_len=kv_len)
+    ws = torch.empty(max(1, attn.load_library().pelica_attn_mla_workspace_bytes(desc)), dtype=torch.uint8,
+                     device="cuda")
+
+    def call(i):
+        attn.mla(q, lats[i], kv_len=kv_len, out=out, workspace=ws)
+
+    ms = time_calls(call, len(lats), steps, warmup)
+    kt = kernel_times(call, len(lats), steps)
+    nbytes = kv_len * 512 * 2 + 2 * q.numel() * 4
+    return dict(config=f"mla_decode_h{n_head}_32k", ms=ms, bytes=nbytes, GBps=nbytes / (ms * 1e-3) / 1e9,
+                frac_hbm=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, kernel_ms=kt)
+
+
+def bench_qkv(steps, warmup, T=4096, n_head=64, n_kv=8, hd=64):
+    """The step before attention over a 4096-token gpt-oss pass: q, k, v f32
+    in, q f32 out, k/v f16 rows out (HBM-bound)."""
+    import torch
+
+    from pelica_amd import attn
+
+    g = torch.Generator(device="cuda").manual_seed(13)
+    q = torch.randn(1, T, n_head, hd, generator=g, device="cuda")
+    k = torch.randn(1, T, n_kv, hd, generator=g, device="cuda")
+    v = torch.randn(1, T, n_kv, hd, generator=g, device="cuda")
+    pos = torch.arange(T, device="cuda", dtype=torch.float64)[:, None]
+    th = pos * 150000.0 ** (-(2.0 * torch.arange(hd // 2, device="cuda", dtype=torch.float64)) / hd)
+    table = torch.stack([th.cos(), th.sin()], -1).float().contiguous()
+    kc = torch.empty(T, n_kv * hd, dtype=torch.float16, device="cuda")
+    vc = torch.empty_like(kc)
+
+    def call(i):
+        attn.qkv_rope_cache(q, k, v, kc, vc, n_kv=n_kv, kv_len=T, table=table)
+
+    ms = time_calls(call, 1, steps, warmup)
+    kt = kernel_times(call, 1, steps)
+    nbytes = q.numel() * 4 * 2 + (k.numel() + v.numel()) * (4 + 2) + T * (hd // 2) * 8
+    return dict(config="qkv_rope_cache_gptoss_4096", ms=ms, bytes=nbytes, GBps=nbytes / (ms * 1e-3) / 1e9,
+                frac_hbm=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, kernel_ms=kt)
+
+
 def cpu_baseline_decode(cfg, reps=5):
     """The C port of cpu_attn.rs on every host core, full C3 workload."""
     import numpy as np
@@ -270,6 +323,11 @@ def main():
     for cfg in (wl.C4_FULL, wl.C4_SWA):
         if want(cfg):
             results[cfg.name] = bench_prefill(cfg, args.steps, args.warmup)
+    # the path's other kernels (no BASELINE config of their own)
+    if not only or "mla_decode_h32_32k" in only:
+        results["mla_decode_h32_32k"] = bench_mla(args.steps, args.warmup)
+    if not only or "qkv_rope_cache_gptoss_4096" in only:
+        results["qkv_rope_cache_gptoss_4096"] = bench_qkv(args.steps, args.warmup)
 
     head = results.get(wl.C3_FULL.name)
     pre = results.get(wl.C4_FULL.name)

@@ -61,6 +61,28 @@ __device__ __forceinline__ half8 load16(const void* p) {
     return __builtin_bit_cast(half8, *reinterpret_cast<const u32x4*>(p));
 }
 
+// Workgroup barrier for LDS data only: waits for this wave's own LDS
+// operations (lgkmcnt(0)), not for vector-memory loads — __syncthreads()'s
+// fence would also wait for every in-flight buffer_load ... lds (vmcnt(0)),
+// draining a prefetch pipeline; kernels that stream tiles into LDS wait for
+// those explicitly.  The empty asm keeps the compiler from moving memory
+// accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt, expcnt untouched (max)
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+}
+
+// 16 bytes per lane from a buffer resource straight into LDS at
+// lds_base + 16 * lane (buffer_load_dwordx4 ... lds, base in M0).  Callers
+// wait for these loads (s_waitcnt vmcnt) before the barrier that publishes
+// the tile.
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset, void* lds_base) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)lds_base, 16, voffset, 0,
+                                             0, 0);
+}
+
 // Split x into f16 hi + lo with x ~= hi + lo to ~2^-22 relative.
 __device__ __forceinline__ void split_f16(float x, _Float16& hi, _Float16& lo) {
     hi = (_Float16)x;

@@ -414,14 +414,16 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
 // are issued before the (max, sum) pass so both are in flight together.
 template <int HD>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
-    constexpr int D4 = HD / 4;
-    constexpr int PH = 256 / D4;        // phases: 16 (hd 64), 8 (hd 128), 2 (hd 512)
+    constexpr int DW = HD < 128 ? HD : 128;  // dims per workgroup (hd 512: four workgroups per row)
+    constexpr int NQ = HD / DW;
+    constexpr int D4 = DW / 4;
+    constexpr int PH = 256 / D4;        // phases: 16 (hd 64), 8 (hd 128 and 512)
     constexpr int J = 16;               // splits per thread per pass
     __shared__ float s_w[kMaxSlots];
     __shared__ float s_red[256 / 64];
     __shared__ float4v s_o[256];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
+    const int r = blockIdx.x / NQ, dq = blockIdx.x % NQ, kvh = blockIdx.y, s = blockIdx.z;
     const int len = p.seq_len ? p.seq_len[s] : p.kv_len;
     if (len < p.T || len <= 0) return;
     const int lo_min = key_range(len, p.T, 0, p.window).lo;
@@ -432,7 +434,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
     const KeyRange krg = key_range(len, p.T, t, p.window);
     const int c0 = krg.lo / p.split_keys - split0, c1 = min(krg.pos / p.split_keys - split0, n_active - 1);
     const size_t base = ((size_t)(s * p.n_kv + kvh) * p.R + r) * p.n_slot;
-    const int ph = tid / D4, d = 4 * (tid % D4);
+    const int ph = tid / D4, d = 4 * (tid % D4) + DW * dq;
 
     // first pass of O loads, in flight while the weights are computed
     float4v ov[J];
@@ -495,6 +497,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
     s_o[tid] = acc;
     __syncthreads();
     if (tid < D4) {
+        const int d = 4 * tid + DW * dq;
         float4v sum = s_o[tid];
 #pragma unroll
         for (int q = 1; q < PH; ++q) sum += s_o[q * D4 + tid];
@@ -521,7 +524,7 @@ static hipError_t launch_k(const DecodeParams& p, hipStream_t st) {
 
 hipError_t launch_combine(const DecodeParams& p, hipStream_t st) {
     ProfScope ps(kProfDecodeCombine, st);
-    const dim3 grid(p.R, p.n_kv, p.n_seq);
+    const dim3 grid(p.R * (p.hd > 128 ? p.hd / 128 : 1), p.n_kv, p.n_seq);
     switch (p.hd) {
         case 64: hipLaunchKernelGGL(decode_combine_kernel<64>, grid, dim3(256), 0, st, p); break;
         case 128: hipLaunchKernelGGL(decode_combine_kernel<128>, grid, dim3(256), 0, st, p); break;

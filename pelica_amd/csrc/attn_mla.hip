@@ -34,6 +34,10 @@ __device__ __forceinline__ const _Float16* mla_elem(const char* base, int k, int
     return reinterpret_cast<const _Float16*>(base + mla_slot(k, d >> 3) + ((d & 7) << 1));
 }
 
+// s_waitcnt immediate: at most n vector-memory ops outstanding (gfx9
+// encoding: vmcnt[3:0], expcnt[6:4] and lgkmcnt[11:8] left at max, vmcnt[5:4])
+constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
+
 }  // namespace
 
 template <int RT>
@@ -41,10 +45,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     constexpr int HD = kMlaHd, NW = 4, KB = 32;  // dims, waves, keys per block
     constexpr int DS = HD / NW / 32;             // 32-dim k-steps per wave (4)
     constexpr int DT = HD / NW / 16;             // 16-dim output tiles per wave (8)
-    constexpr int ROWS = 16 * RT, NP = 2;
+    constexpr int ROWS = 16 * RT, NP = 2;  // f16 parts of Q (hi + lo: ~fp32 scores)
+#ifndef PELICA_MLA_P_PARTS
+#define PELICA_MLA_P_PARTS 1
+#endif
+    constexpr int NPP = PELICA_MLA_P_PARTS;  // f16 parts of P (the PV weights)
     constexpr int BLK = KB * HD * 2;             // 32 KB
-    __shared__ __attribute__((aligned(16))) char lds[2 * BLK + NW * ROWS * KB * 4];
-    float* const part = reinterpret_cast<float*>(lds + 2 * BLK);  // [NW][ROWS][KB] partial scores
+    constexpr int NBUF = RT == 4 ? 3 : 4;        // latent blocks in the LDS ring
+    constexpr int LPB = KB / NW;                 // loads per block per thread
+    constexpr int PS = KB + 4;  // partial-score row stride in floats: rows land on distinct banks
+    __shared__ __attribute__((aligned(16))) char lds[NBUF * BLK + NW * ROWS * PS * 4];
+    float* const part = reinterpret_cast<float*>(lds + NBUF * BLK);  // [NW][ROWS][PS] partial scores
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
     const int rg = blockIdx.y, s = blockIdx.z, slot = blockIdx.x;
@@ -60,46 +71,51 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const uint32_t stride_b = (uint32_t)p.row_stride * 2;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(p.k + row0 * p.row_stride), (short)0, (int)((uint32_t)len * stride_b), kBufFlags);
-    // block i -> LDS buffer i & 1; wave instruction j of wave w fills key row
-    // 4 j + w (64 slots of 16 bytes); the lane loads the piece its slot holds
+    // block i -> LDS buffer i % NBUF; wave instruction j of wave w fills key
+    // row 4 j + w (64 slots of 16 bytes); the lane loads the piece its slot holds
     auto load_block = [&](int i) {
-        char* dst = lds + (i & 1) * BLK;
+        char* dst = lds + (i % NBUF) * BLK;
         const int kb = kbeg + KB * i;
 #pragma unroll
         for (int j = 0; j < KB / NW; ++j) {
             const int key = NW * j + wave;
             const int piece = lane ^ (key & 15);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rs, (__attribute__((address_space(3))) void*)(dst + key * (HD * 2)), 16,
-                (uint32_t)(kb + key) * stride_b + 16 * piece, 0, 0, 0);
+            lds_dma16(rs, (uint32_t)(kb + key) * stride_b + 16 * piece, dst + key * (HD * 2));
         }
     };
-    load_block(0);
-
-    // queries of this lane's rows, this wave's dims, f16 hi + lo, base 2
-    half8 qf[NP][RT][DS];
+    // queries of this lane's rows, this wave's dims (requested before the
+    // first latent blocks, so waiting for them does not wait for the blocks)
+    float4v qa[RT][DS], qb2[RT][DS];
     int posr[RT];
+    bool qok[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
         const int r = rbase + 16 * rt + c16;
-        const bool ok = r < p.R;
-        const int rr = ok ? r : 0;
+        qok[rt] = r < p.R;
+        const int rr = qok[rt] ? r : 0;
         const int t = rr / p.hpk, h = rr % p.hpk;
         const float* qp = p.q + ((size_t)(s * p.T + t) * p.n_head + h) * HD + 128 * wave + 8 * g;
-        posr[rt] = ok ? len - p.T + t : -1;
+        posr[rt] = qok[rt] ? len - p.T + t : -1;
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds) {
-            const float4v a = *reinterpret_cast<const float4v*>(qp + 32 * ds);
-            const float4v b = *reinterpret_cast<const float4v*>(qp + 32 * ds + 4);
+            qa[rt][ds] = *reinterpret_cast<const float4v*>(qp + 32 * ds);
+            qb2[rt][ds] = *reinterpret_cast<const float4v*>(qp + 32 * ds + 4);
+        }
+    }
+    for (int i = 0; i < NBUF - 1 && i < nblk; ++i) load_block(i);
+    // f16 hi + lo parts, base 2
+    half8 qf[NP][RT][DS];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds)
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float x = ok ? (j < 4 ? a[j] : b[j - 4]) * p.qscale : 0.f;
+                const float x = qok[rt] ? (j < 4 ? qa[rt][ds][j] : qb2[rt][ds][j - 4]) * p.qscale : 0.f;
                 const _Float16 hi = (_Float16)x;
                 qf[0][rt][ds][j] = hi;
                 qf[1][rt][ds][j] = (_Float16)(x - (float)hi);
             }
-        }
-    }
 
     float m[RT], l[RT];
     float4v o[DT][RT];
@@ -112,10 +128,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
 
     for (int i = 0; i < nblk; ++i) {
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): block i is in LDS
-        __syncthreads();                     // ... for every wave; block i-1's readers are done
-        if (i + 1 < nblk) load_block(i + 1);
-        const char* blk = lds + (i & 1) * BLK;
+        // block i is in LDS once at most the loads of the blocks issued after
+        // it are outstanding (loads complete in order)
+        const int later = min(nblk - 1 - i, NBUF - 2);
+        if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * LPB));
+        else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPB));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        lds_barrier();  // ... for every wave; block i-1's readers are done
+        if (i + NBUF - 1 < nblk) load_block(i + NBUF - 1);  // into block i-1's buffer
+        const char* blk = lds + (i % NBUF) * BLK;
         const int kb = kbeg + KB * i;
 
         // partial scores over this wave's dims: 2 key tiles x RT row tiles
@@ -144,9 +165,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt)
-                *reinterpret_cast<float4v*>(part + (wave * ROWS + 16 * rt + c16) * KB + 16 * kt + 4 * g) =
+                *reinterpret_cast<float4v*>(part + (wave * ROWS + 16 * rt + c16) * PS + 16 * kt + 4 * g) =
                     acc[0][kt][rt] + acc[1][kt][rt];
-        __syncthreads();
+        lds_barrier();
         float4v sc[2][RT];
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
@@ -155,33 +176,54 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 float4v t4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int w = 0; w < NW; ++w)
-                    t4 += *reinterpret_cast<const float4v*>(part + (w * ROWS + 16 * rt + c16) * KB + 16 * kt + 4 * g);
+                    t4 += *reinterpret_cast<const float4v*>(part + (w * ROWS + 16 * rt + c16) * PS + 16 * kt + 4 * g);
                 sc[kt][rt] = t4;
             }
 
-        // causal mask and online softmax (identical in every wave)
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int key = kb + 16 * kt + 4 * g + e;
-#pragma unroll
-                for (int rt = 0; rt < RT; ++rt)
-                    if (key >= kend || key > posr[rt]) sc[kt][rt][e] = -INFINITY;
-            }
-        half8 pf[NP][RT];
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-            float bm = -INFINITY;
+        // causal mask (only the blocks that reach past a row's position or
+        // the split) and online softmax, identical in every wave; the running
+        // max moves (O and l rescaled) only when a row's block max exceeds it
+        // by 2^8, so most blocks skip the rescale
+        if (kb + KB > kend || kb + KB - 1 > posr[0]) {
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) bm = fmaxf(bm, sc[kt][rt][e]);
-            bm = group4_max(bm);
-            const float mn = fmaxf(m[rt], bm);
-            const float ms = (mn == -INFINITY) ? 0.f : mn;
-            const float c = fast_exp2(m[rt] - ms);
-            m[rt] = mn;
+                for (int e = 0; e < 4; ++e) {
+                    const int key = kb + 16 * kt + 4 * g + e;
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt)
+                        if (key >= kend || key > posr[rt]) sc[kt][rt][e] = -INFINITY;
+                }
+        }
+        float bm[RT];
+        bool grow = false;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            float x = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) x = fmaxf(x, sc[kt][rt][e]);
+            bm[rt] = group4_max(x);
+            grow |= bm[rt] > m[rt] + 8.f;
+        }
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const float mn = fmaxf(m[rt], bm[rt]);
+                if (mn > m[rt]) {
+                    const float c = fast_exp2(m[rt] - mn);  // 0 when m was -inf
+                    l[rt] *= c;
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt) o[dt][rt] *= c;
+                    m[rt] = mn;
+                }
+            }
+        }
+        half8 pf[NPP][RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            const float ms = m[rt] == -INFINITY ? 0.f : m[rt];
             float ls = 0.f;
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt)
@@ -191,11 +233,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                     ls += pe;
                     const _Float16 hi = (_Float16)pe;
                     pf[0][rt][kt * 4 + e] = hi;
-                    pf[1][rt][kt * 4 + e] = (_Float16)(pe - (float)hi);
+                    if (NPP > 1) pf[NPP - 1][rt][kt * 4 + e] = (_Float16)(pe - (float)hi);
                 }
-            l[rt] = l[rt] * c + ls;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) o[dt][rt] *= c;
+            l[rt] += ls;
         }
 
         // O^T[this wave's dims] += V^T P^T (keys in the B operand's order)
@@ -204,7 +244,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             const int k0 = 4 * g + (c16 >> 2), d0 = 128 * wave + 16 * dt + 4 * (c16 & 3);
             const half8 va = cat8(lds_read_tr(mla_elem(blk, k0, d0)), lds_read_tr(mla_elem(blk, k0 + 16, d0)));
 #pragma unroll
-            for (int pp = 0; pp < NP; ++pp)
+            for (int pp = 0; pp < NPP; ++pp)
 #pragma unroll
                 for (int rt = 0; rt < RT; ++rt) o[dt][rt] = mfma16(va, pf[pp][rt], o[dt][rt]);
         }

@@ -127,8 +127,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             // (round rows before key_begin wrap to offsets past nrec: zeros)
             const uint32_t off = RING ? ((kb + key) % p.ring_cap) * stride_b + 16 * piece
                                       : (uint32_t)(kb + key - kbeg) * stride_b + 16 * piece;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rs, (__attribute__((address_space(3))) void*)(dst + 1024 * (NW * i + wave)), 16, off, 0, 0, 0);
+            lds_dma16(rs, off, dst + 1024 * (NW * i + wave));
         }
     };
     // s_waitcnt vmcnt(0): the tile loads above have landed in LDS
