@@ -53,12 +53,15 @@ __device__ __forceinline__ float wave_sum(float x) {
     return x;
 }
 
+#ifndef PELICA_DEXP
+#define PELICA_DEXP 0
+#endif
 #ifndef PELICA_DEPTH64
 #define PELICA_DEPTH64 1
 #endif
 // waves per SIMD the decode kernel is compiled for (register budget 512/n)
 template <int HD, int RT, int NW>
-constexpr int kDecodeOcc = NW == 8 ? 2 : HD == 64 ? (RT == 1 ? 3 : RT == 2 ? 2 : 1) : 1;
+constexpr int kDecodeOcc = NW == 8 ? 2 : HD == 64 ? (RT <= 2 ? 2 : 1) : 1;
 
 // f16 parts the decode kernel splits Q and P into: 2 (hi + lo, ~fp32
 // products) or 1 (f16 only)
@@ -70,6 +73,13 @@ constexpr int kDecodeSplitParts = PELICA_DECODE_PARTS;
 // blocks in flight per wave (register budget)
 template <int HD, int RT>
 constexpr int kDecodeDepth = (HD == 64 && RT == 1) ? PELICA_DEPTH64 : 1;
+
+// cache policy bits of the K/V stream loads: nt (streaming, the cache lines
+// are not kept) — each K/V byte is read once
+#ifndef PELICA_DECODE_AUX
+#define PELICA_DECODE_AUX 2
+#endif
+constexpr int kKvAux = PELICA_DECODE_AUX;
 
 // word 3 of a gfx9 buffer resource: 32-bit data format, raw addressing
 constexpr int kBufferFlags = 0x00020000;
@@ -106,17 +116,43 @@ __device__ __forceinline__ void store_part(float* slot, int d, float m2, float l
     *reinterpret_cast<float2*>(slot + 4 + d) = make_float2(o[2], o[3]);
 }
 
-template <int HD, int RT, int NW, int H, bool RING, int D>
+// K blocks in LDS: 16-byte piece p of key row k sits at slot p ^ k_swz(k), so
+// the 16 keys that one ds_read_b128 of the QK^T A operand touches (same
+// piece) fall in distinct banks, and the 8 (hd 64) or 4 (hd 128) keys of one
+// full-line global load keep a per-lane swizzle that differs between loads
+// only by a constant (k_swz_j).
+template <int HD>
+__device__ __forceinline__ int k_swz(int k) {
+    return HD == 64 ? (((k >> 1) ^ ((k & 1) << 2)) & 7) : (k & 15);
+}
+// k_swz(KPL * j + k0) == k_swz(k0) ^ k_swz_j(j) for k0 < KPL (KPL = keys per
+// 64-lane load: 8 for hd 64, 4 for hd 128)
+template <int HD>
+__device__ constexpr int k_swz_j(int j) {
+    return HD == 64 ? 4 * (j & 1) : (4 * j) & 15;
+}
+
+// the value of lane l ^ 8 (within each 16-lane row)
+__device__ __forceinline__ float ror8(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, false));
+}
+
+template <int HD, int RT, int NW, int H, bool RING, int D, bool PK>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecodeOcc<HD, RT, NW>, 8))) void decode_kernel(DecodeParams p) {
+    static_assert(!PK || RT == 1, "packed hi/lo columns need one row tile");
     constexpr int DS = HD / 32;   // 32-dim k-steps of the QK^T MFMA
     constexpr int DT = HD / 16;   // 16-dim output tiles
-    constexpr int VPL = HD / 8;   // 16-byte V pieces per lane per block
+    constexpr int VPL = HD / 8;   // 16-byte pieces per lane per block, each of K and V
     constexpr int ROWS = RT * 16;
-    constexpr int NP = kDecodeSplitParts;              // f16 parts of Q and P (hi, lo)
-    constexpr int VBUF = 64 * HD * 2;                  // bytes of one wave's V block
-    constexpr int MERGE = NW * ROWS * (HD + 2) * 4;    // bytes of the wave-merge area
-    constexpr int SMEM = VBUF * NW > MERGE ? VBUF * NW : MERGE;
+    // f16 parts of Q and P: packed (PK: hi in columns 0-7, lo in 8-15, one
+    // MFMA), or NP separate passes
+    constexpr int NP = PK ? 1 : kDecodeSplitParts;
+    constexpr int BUF = 64 * HD * 2;                   // bytes of one 64-key K or V block
+    constexpr int STATE = DT * RT * 64 * 16 + RT * 64 * 8;  // bytes of one wave's (O, m, l)
+    constexpr int WSLOT = 2 * BUF > STATE ? 2 * BUF : STATE;   // LDS per wave: K and V block, then state
+    constexpr int SMEM = WSLOT * NW;
     __shared__ __attribute__((aligned(16))) char smem[SMEM];
+    __shared__ unsigned arrivals[H];  // waves of each head done (merge at the end)
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
     constexpr int W = NW / H;                   // waves per head
@@ -148,65 +184,53 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
         (void*)(p.k + row0 * p.row_stride + (size_t)kvh * HD), (short)0, (int)nrec, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(p.v + row0 * p.row_stride + (size_t)kvh * HD), (short)0, (int)nrec, kBufferFlags);
-    // V piece slot i*64+lane of a block holds key i*KPL + lane/PPR and the
-    // swizzled 16-byte piece of lane%PPR; the key's low two bits (the
-    // swizzle) depend on the lane only, so one lane offset serves every i
+    // Both K and V are fetched in whole 128-byte lines: load j of a block
+    // gives lane l key KPL*j + l/PPR, piece l%PPR, and the lane's 16 bytes go
+    // to LDS slot j*64 + l of the wave's buffer.  The lane reads the logical
+    // piece that belongs in that slot under the buffer's swizzle: V
+    // (v_slot) depends on the key's low two bits (the lane's own), K
+    // (k_swz) on more, through a per-load constant.
     constexpr int PPR = HD / 8;         // 16-byte pieces per key row
     constexpr int KPL = 64 / PPR;       // keys per 64 lanes
     const int vk0 = lane / PPR;
     const uint32_t vcol = 16 * ((lane % PPR) ^ ((vk0 & 3) << 1));
+    const uint32_t kcol0 = (lane % PPR) ^ k_swz<HD>(vk0);
     // this wave's blocks: kb = kfirst + 64 * (wsub + W * i)
     int kfirst = kbeg;
     if (lo_min > kbeg) kfirst = kbeg + ((lo_min - kbeg) & ~63);
     const int nblk_all = (kend - kfirst + 63) / 64;
     const int nb = nblk_all > wsub ? (nblk_all - wsub + W - 1) / W : 0;
-    char* vlds = smem + wave * VBUF;
+    char* klds = smem + wave * WSLOT;
+    char* vlds = klds + BUF;
     auto blk = [&](int i) { return kfirst + 64 * (wsub + W * i); };
 
-    // D blocks in flight: K straight into MFMA-operand registers, V into
-    // staging registers
-    half8 kr[D][4][DS];
-    u32x4 vr[D][VPL];
-    auto issue = [&](half8 (&kd)[4][DS], u32x4 (&vd)[VPL], int i) {
+    // D blocks in flight in staging registers
+    u32x4 kr[D][VPL], vr[D][VPL];
+    auto issue = [&](u32x4 (&kd)[VPL], u32x4 (&vd)[VPL], int i) {
         const bool valid = i < nb;
         const int kb = blk(i);
-        if (!RING) {
-            const uint32_t base = valid ? (uint32_t)kb * stride_b : nrec;
 #pragma unroll
-            for (int j = 0; j < VPL; ++j)
-                vd[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                      rv, base + (KPL * j + vk0) * stride_b + vcol, 0, 0));
-#pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-                for (int ds = 0; ds < DS; ++ds)
-                    kd[kt][ds] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(
-                                                               rk, base + (16 * kt + c16) * stride_b + 16 * g + 64 * ds,
-                                                               0, 0));
-        } else {
-#pragma unroll
-            for (int j = 0; j < VPL; ++j) {
-                const uint32_t off = valid ? ((kb + KPL * j + vk0) % p.ring_cap) * stride_b + vcol : nrec;
-                vd[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
-            }
-#pragma unroll
-            for (int kt = 0; kt < 4; ++kt) {
-                const uint32_t off = valid ? ((kb + 16 * kt + c16) % p.ring_cap) * stride_b + 16 * g : nrec;
-#pragma unroll
-                for (int ds = 0; ds < DS; ++ds)
-                    kd[kt][ds] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rk, off + 64 * ds, 0, 0));
-            }
+        for (int j = 0; j < VPL; ++j) {
+            uint32_t row;
+            if (!RING) row = valid ? (uint32_t)(kb + KPL * j + vk0) * stride_b : nrec;
+            else row = valid ? (uint32_t)((kb + KPL * j + vk0) % p.ring_cap) * stride_b : nrec;
+            kd[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  rk, row + 16 * (kcol0 ^ k_swz_j<HD>(j)), 0, kKvAux));
+            vd[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, row + vcol, 0, kKvAux));
         }
     };
 #pragma unroll
     for (int sl = 0; sl < D; ++sl) issue(kr[sl], vr[sl], sl);
 
     // ---- queries of this lane's rows: f16 parts (hi[, lo]) in base 2 ----
+    // PK: column c16 < 8 holds the hi part of row c16, column c16 + 8 its lo
+    // part; the two partial scores are summed across lanes l, l ^ 8.
     half8 qf[NP][RT][DS];
     int posr[RT], lor[RT];
+    int lo_hi = 0, pos_lo = INT32_MAX;  // keys every valid row of the wave sees
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-        const int r = rbase + 16 * rt + c16;
+        const int r = rbase + 16 * rt + (PK ? (c16 & 7) : c16);
         const bool rv_ok = r < p.R;
         const int rr = rv_ok ? r : 0;
         const int t = rr / p.hpk, h = kvh * p.hpk + rr % p.hpk;
@@ -214,6 +238,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
         const KeyRange krg = key_range(len, p.T, t, p.window);
         posr[rt] = rv_ok ? krg.pos : -1;
         lor[rt] = krg.lo;
+        if (rv_ok) {
+            lo_hi = max(lo_hi, krg.lo);
+            pos_lo = min(pos_lo, krg.pos);
+        }
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds) {
             const float4v a = *reinterpret_cast<const float4v*>(qp + 32 * ds);
@@ -222,10 +250,26 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
             for (int j = 0; j < 8; ++j) {
                 const float x = rv_ok ? (j < 4 ? a[j] : b[j - 4]) * p.qscale : 0.f;
                 const _Float16 hi = (_Float16)x;
-                qf[0][rt][ds][j] = hi;
-                if (NP > 1) qf[NP - 1][rt][ds][j] = (_Float16)(x - (float)hi);
+                const _Float16 lo = (_Float16)(x - (float)hi);
+                if (PK) {
+                    qf[0][rt][ds][j] = c16 < 8 ? hi : lo;
+                } else {
+                    qf[0][rt][ds][j] = hi;
+                    if (NP > 1) qf[NP - 1][rt][ds][j] = lo;
+                }
             }
         }
+    }
+    if (W > 1) {
+        // the arrival counters are set before any wave can count itself in
+        if (tid < H) arrivals[tid] = 0;
+        lds_barrier();
+    }
+    // wave-uniform bounds: blocks inside [lo_hi, pos_lo] need no mask
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        lo_hi = max(lo_hi, __shfl_xor(lo_hi, off, 64));
+        pos_lo = min(pos_lo, __shfl_xor(pos_lo, off, 64));
     }
 
     float m[RT], l[RT];
@@ -238,15 +282,35 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
         for (int dt = 0; dt < DT; ++dt) o[dt][rt] = float4v{0.f, 0.f, 0.f, 0.f};
     }
 
-    auto stage_v = [&](const u32x4 (&vs)[VPL]) {
-        // previous block's transposed reads are done (in-order LDS, same wave)
+    auto stage = [&](const u32x4 (&ks)[VPL], const u32x4 (&vs)[VPL]) {
+        // the previous block's LDS reads are done (in-order LDS, same wave)
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) *reinterpret_cast<u32x4*>(vlds + (j * 64 + lane) * 16) = vs[j];
+        for (int j = 0; j < VPL; ++j) {
+            *reinterpret_cast<u32x4*>(klds + (j * 64 + lane) * 16) = ks[j];
+            *reinterpret_cast<u32x4*>(vlds + (j * 64 + lane) * 16) = vs[j];
+        }
         __builtin_amdgcn_wave_barrier();
     };
+    // A operand of k-step ds for key tile kt: key 16 kt + c16 (k_swz of it
+    // is k_swz(c16)), logical piece g + 4 ds
+    const char* kread[DS];
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) kread[ds] = klds + c16 * (HD * 2) + 16 * ((g + 4 * ds) ^ k_swz<HD>(c16));
     float4v sc[4][RT];
-    auto qk = [&](const half8 (&kc)[4][DS]) {
+    auto qk = [&]() {
+#if PELICA_DEXP & 1
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) sc[kt][rt] = float4v{(float)klds[lane + kt], 0.f, 0.f, 0.f};
+        return;
+#endif
+        half8 kc[4][DS];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int ds = 0; ds < DS; ++ds) kc[kt][ds] = load16(kread[ds] + kt * 16 * (HD * 2));
         // independent accumulators per (part, key tile, row tile); the
         // k-steps run outermost so consecutive MFMAs do not depend on each other
         float4v acc[NP][4][RT];
@@ -267,19 +331,32 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt) sc[kt][rt] = NP > 1 ? acc[0][kt][rt] + acc[NP - 1][kt][rt] : acc[0][kt][rt];
+            for (int rt = 0; rt < RT; ++rt) {
+                if (PK) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) sc[kt][rt][i] = acc[0][kt][rt][i] + ror8(acc[0][kt][rt][i]);
+                } else {
+                    sc[kt][rt] = NP > 1 ? acc[0][kt][rt] + acc[NP - 1][kt][rt] : acc[0][kt][rt];
+                }
+            }
     };
     auto softmax_pv = [&](int kb) {
-        // mask: row r sees keys [lor, posr]
+#if PELICA_DEXP & 2
+        o[0][0] += sc[0][0] + sc[3][RT-1] + float4v{(float)*reinterpret_cast<const _Float16*>(vlds + lane * 16), 0.f, 0.f, 0.f};
+        return;
+#endif
+        // mask (blocks at a range boundary only): row r sees keys [lor, posr]
+        if (kb < lo_hi || kb + 63 > pos_lo) {
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+            for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int key = kb + 16 * kt + 4 * g + i;
+                for (int i = 0; i < 4; ++i) {
+                    const int key = kb + 16 * kt + 4 * g + i;
 #pragma unroll
-                for (int rt = 0; rt < RT; ++rt)
-                    if (key < lor[rt] || key > posr[rt]) sc[kt][rt][i] = -INFINITY;
-            }
+                    for (int rt = 0; rt < RT; ++rt)
+                        if (key < lor[rt] || key > posr[rt]) sc[kt][rt][i] = -INFINITY;
+                }
+        }
         half8 pf[NP][RT][2];
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
@@ -301,8 +378,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
                     const float pe = fast_exp2(sc[kt][rt][i] - ms);
                     ls += pe;
                     const _Float16 hi = (_Float16)pe;
-                    pf[0][rt][kt >> 1][(kt & 1) * 4 + i] = hi;
-                    if (NP > 1) pf[NP - 1][rt][kt >> 1][(kt & 1) * 4 + i] = (_Float16)(pe - (float)hi);
+                    const int e = (kt & 1) * 4 + i;
+                    if (PK) {
+                        pf[0][rt][kt >> 1][e] = c16 < 8 ? hi : (_Float16)(pe - (float)hi);
+                    } else {
+                        pf[0][rt][kt >> 1][e] = hi;
+                        if (NP > 1) pf[NP - 1][rt][kt >> 1][e] = (_Float16)(pe - (float)hi);
+                    }
                 }
             l[rt] = l[rt] * c + ls;
 #pragma unroll
@@ -334,61 +416,91 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
 #pragma unroll
         for (int sl = 0; sl < D; ++sl) {
             if (i + sl < nb) {
-                stage_v(vr[sl]);
-                qk(kr[sl]);
+                stage(kr[sl], vr[sl]);
                 issue(kr[sl], vr[sl], i + sl + D);
+                qk();
                 softmax_pv(blk(i + sl));
             }
         }
     }
+    if (PK) {
+        // columns c16 and c16 ^ 8 hold the hi and lo parts of one row
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[dt][0][i] += ror8(o[dt][0][i]);
+    }
 
-    // ---- merge the W wave states of each (head, row) through LDS ----
+    // ---- merge the W wave states of each head ----
+    // No workgroup barrier: each wave leaves its state (m, l, O) in its own
+    // K/V buffer (free after its last block) and counts itself in on its
+    // head's LDS counter; the wave that arrives last merges the W states in
+    // wave order and writes the result.  LDS operations of one wave complete
+    // in order, so a wave's state is in place before its count.
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) l[rt] = group4_sum(l[rt]);
-    __syncthreads();  // V buffers are free
-    float* mo = reinterpret_cast<float*>(smem);            // [NW][ROWS][HD] O
-    float* mml = mo + NW * ROWS * HD;                       // [NW][ROWS][2] (m, l)
+    float4v* st_o = reinterpret_cast<float4v*>(klds);               // [DT][RT][64 lanes]
+    float2* st_ml = reinterpret_cast<float2*>(klds + DT * RT * 64 * 16);  // [RT][64 lanes]
+    auto state_of = [&](int w) {
+        return reinterpret_cast<char*>(smem) + (w * H + hl) * WSLOT;
+    };
+    if (W > 1) {
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) st_o[(dt * RT + rt) * 64 + lane] = o[dt][rt];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) st_ml[rt * 64 + lane] = make_float2(m[rt], l[rt]);
+        unsigned prev = 0;
+        if (lane == 0)
+            prev = __hip_atomic_fetch_add(&arrivals[hl], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+        prev = __builtin_amdgcn_readfirstlane(prev);
+        if (prev != W - 1) return;
+        // last of the head's waves: merge all W states in wave order
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            float mw[W], lw[W];
+            float M = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < W; ++w) {
+                const float2 ml = reinterpret_cast<const float2*>(state_of(w) + DT * RT * 64 * 16)[rt * 64 + lane];
+                mw[w] = ml.x;
+                lw[w] = ml.y;
+                M = fmaxf(M, ml.x);
+            }
+            const float ms = (M == -INFINITY) ? 0.f : M;
+            float L = 0.f;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o[dt][rt] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int w = 0; w < W; ++w) {
+                const float wt = fast_exp2(mw[w] - ms);
+                L += lw[w] * wt;
+                const float4v* so = reinterpret_cast<const float4v*>(state_of(w));
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) o[dt][rt] += so[(dt * RT + rt) * 64 + lane] * wt;
+            }
+            m[rt] = M;
+            l[rt] = L;
+        }
+    }
+
+    // this lane's result: row 16 rt + c16 (PK: c16 < 8), dims 16 dt + 4 g
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
         const int row = 16 * rt + c16;
-        float* dst = mo + (wave * ROWS + row) * HD + 4 * g;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<float4v*>(dst + 16 * dt) = o[dt][rt];
-        if (g == 0) {
-            mml[(wave * ROWS + row) * 2] = m[rt];
-            mml[(wave * ROWS + row) * 2 + 1] = l[rt];
-        }
-    }
-    __syncthreads();
-
-    const int rows_here = min(ROWS, p.R - rbase);
-    // (head, row, 4-dim chunk) items of the workgroup's result; wave
-    // wsub * H + h holds phase wsub of head h
-    constexpr int D4 = HD / 4;
-    for (int it = tid; it < H * rows_here * D4; it += 64 * NW) {
-        const int h_l = it / (rows_here * D4), rest = it % (rows_here * D4);
-        const int row = rest / D4, d = 4 * (rest % D4);
-        const int kvh_o = (blockIdx.y % hgroups) * H + h_l;
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < W; ++w) M = fmaxf(M, mml[((w * H + h_l) * ROWS + row) * 2]);
-        const float ms = (M == -INFINITY) ? 0.f : M;
-        float L = 0.f;
-        float4v O = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int w = 0; w < W; ++w) {
-            const int src = (w * H + h_l) * ROWS + row;
-            const float wt = fast_exp2(mml[src * 2] - ms);
-            L += mml[src * 2 + 1] * wt;
-            O += *reinterpret_cast<const float4v*>(mo + src * HD + d) * wt;
-        }
         const int r = rbase + row;
+        if ((PK && c16 >= 8) || r >= p.R) continue;
+        const float M = m[rt], L = l[rt];
+        const int t = r / p.hpk, h = kvh * p.hpk + r % p.hpk;
         if (n_active == 1 && p.parts) {
-            const int t = r / p.hpk, h = kvh_o * p.hpk + r % p.hpk;
-            store_part(p.parts + ((size_t)(s * p.T + t) * p.n_head + h) * (HD + 2), d, M, L, O);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+                store_part(p.parts + ((size_t)(s * p.T + t) * p.n_head + h) * (HD + 2), 16 * dt + 4 * g, M, L, o[dt][rt]);
         } else if (n_active == 1) {
             // the only split: normalise here, sink in max and denominator
-            const int t = r / p.hpk, h = kvh_o * p.hpk + r % p.hpk;
+            const float ms = (M == -INFINITY) ? 0.f : M;
             float f;
             if (p.sinks) {
                 const float sk = p.sinks[h] * kLog2e;
@@ -398,11 +510,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
             } else {
                 f = 1.f / L;
             }
-            *reinterpret_cast<float4v*>(p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + d) = O * f;
+            float* op = p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + 4 * g;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<float4v*>(op + 16 * dt) = o[dt][rt] * f;
         } else {
-            const size_t idx = ((size_t)(s * p.n_kv + kvh_o) * p.R + r) * p.n_slot + slot;
-            if (d == 0) *reinterpret_cast<float2*>(p.ws_ml + 2 * idx) = make_float2(M, L);
-            *reinterpret_cast<float4v*>(p.ws_o + idx * HD + d) = O;
+            const size_t idx = ((size_t)(s * p.n_kv + kvh) * p.R + r) * p.n_slot + slot;
+            if (g == 0) *reinterpret_cast<float2*>(p.ws_ml + 2 * idx) = make_float2(M, L);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<float4v*>(p.ws_o + idx * HD + 16 * dt + 4 * g) = o[dt][rt];
         }
     }
 }
@@ -514,8 +629,15 @@ static hipError_t launch_k(const DecodeParams& p, hipStream_t st) {
     constexpr int D = kDecodeDepth<HD, RT>;
     {
     ProfScope ps(kProfDecodeSplit, st);
-    if (p.ring_cap) hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, true, D>), grid, dim3(64 * NW), 0, st, p);
-    else hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, false, D>), grid, dim3(64 * NW), 0, st, p);
+    // up to 8 rows per kv head: hi and lo parts share one MFMA (packed columns)
+    const bool pk = RT == 1 && p.R <= 8;
+    if (p.ring_cap) {
+        if (pk) hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, true, D, RT == 1>), grid, dim3(64 * NW), 0, st, p);
+        else hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, true, D, false>), grid, dim3(64 * NW), 0, st, p);
+    } else {
+        if (pk) hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, false, D, RT == 1>), grid, dim3(64 * NW), 0, st, p);
+        else hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, false, D, false>), grid, dim3(64 * NW), 0, st, p);
+    }
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.n_slot == 1) return e;
