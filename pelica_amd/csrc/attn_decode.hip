@@ -154,7 +154,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     __shared__ __attribute__((aligned(16))) char smem[SMEM];
     __shared__ unsigned arrivals[H];  // waves of each head done (merge at the end)
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+    // wave index as a scalar: the buffer resources built from it stay in SGPRs
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4,
+              c16 = lane & 15;
     constexpr int W = NW / H;                   // waves per head
     const int hl = wave % H, wsub = wave / H;   // this wave's head (local) and block phase
     const int hgroups = p.n_kv / H;
@@ -524,19 +526,20 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
 
 // Combine of the split partials of one query row, in key order, with the
 // head's sink (merge_dec, src/moe_kernels.rs:585-617; ATTN_M,
-// src/oss_batch.rs:395-425).  Grid (R, n_kv, n_seq), 256 threads: thread
-// (phase, 4-dim chunk) sums the splits c = phase (mod phases); the O loads
-// are issued before the (max, sum) pass so both are in flight together.
+// src/oss_batch.rs:395-425).  Grid (R x dim quarters, n_kv, n_seq), 256
+// threads; thread (phase, 4-dim chunk) merges the splits c = phase (mod
+// phases) online (running max, rescaled sum), all of its loads in flight
+// at once; the phases of a wave merge through lane exchanges, the four
+// waves through LDS, in a fixed order.
 template <int HD>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
     constexpr int DW = HD < 128 ? HD : 128;  // dims per workgroup (hd 512: four workgroups per row)
     constexpr int NQ = HD / DW;
     constexpr int D4 = DW / 4;
     constexpr int PH = 256 / D4;        // phases: 16 (hd 64), 8 (hd 128 and 512)
-    constexpr int J = 16;               // splits per thread per pass
-    __shared__ float s_w[kMaxSlots];
-    __shared__ float s_red[256 / 64];
-    __shared__ float4v s_o[256];
+    constexpr int J = 8;                // splits per thread per pass
+    __shared__ float4v s_o[4][D4];
+    __shared__ float2 s_ml[4][D4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = blockIdx.x / NQ, dq = blockIdx.x % NQ, kvh = blockIdx.y, s = blockIdx.z;
     const int len = p.seq_len ? p.seq_len[s] : p.kv_len;
@@ -550,76 +553,91 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
     const int c0 = krg.lo / p.split_keys - split0, c1 = min(krg.pos / p.split_keys - split0, n_active - 1);
     const size_t base = ((size_t)(s * p.n_kv + kvh) * p.R + r) * p.n_slot;
     const int ph = tid / D4, d = 4 * (tid % D4) + DW * dq;
+    // the sink logit is requested now, not after the merge
+    const float sk = (p.sinks && !p.parts && tid < D4) ? p.sinks[h] * kLog2e : -INFINITY;
 
-    // first pass of O loads, in flight while the weights are computed
-    float4v ov[J];
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-        const int c = c0 + ph + PH * j;
-        ov[j] = c <= c1 ? *reinterpret_cast<const float4v*>(p.ws_o + (base + c) * HD + d) : float4v{0.f, 0.f, 0.f, 0.f};
-    }
-    // (max, sum) of the row's splits, read once into registers
-    constexpr int MLJ = kMaxSlots / 256;
-    float2 ml[MLJ];
-#pragma unroll
-    for (int j = 0; j < MLJ; ++j) {
-        const int c = c0 + tid + 256 * j;
-        ml[j] = c <= c1 ? *reinterpret_cast<const float2*>(p.ws_ml + 2 * (base + c)) : make_float2(-INFINITY, 0.f);
-    }
-    const float sk = (p.sinks && !p.parts) ? p.sinks[h] * kLog2e : -INFINITY;
-    float M = sk;
-#pragma unroll
-    for (int j = 0; j < MLJ; ++j) M = fmaxf(M, ml[j].x);
-    M = wave_max(M);
-    if (lane == 0) s_red[wave] = M;
-    __syncthreads();
-    M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-    const float ms = (M == -INFINITY) ? 0.f : M;
-    float L = 0.f;
-#pragma unroll
-    for (int j = 0; j < MLJ; ++j) {
-        const int c = c0 + tid + 256 * j;
-        const float wc = fast_exp2(ml[j].x - ms);
-        if (c <= c1) s_w[c - c0] = wc;
-        L += ml[j].y * wc;
-    }
-    L = wave_sum(L);
-    __syncthreads();
-    if (lane == 0) s_red[wave] = L;
-    __syncthreads();
-    L = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
-    if (p.sinks && !p.parts) L += fast_exp2(sk - ms);
-
-    float4v acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-        const int c = c0 + ph + PH * j;
-        if (c <= c1) acc += ov[j] * s_w[c - c0];
-    }
-    for (int cb = c0 + PH * J; cb <= c1; cb += PH * J) {
+    float m = -INFINITY, l = 0.f;
+    float4v o = {0.f, 0.f, 0.f, 0.f};
+    for (int cb = c0; cb <= c1; cb += PH * J) {
+        float2 ml[J];
+        float4v ov[J];
 #pragma unroll
         for (int j = 0; j < J; ++j) {
             const int c = cb + ph + PH * j;
-            ov[j] = c <= c1 ? *reinterpret_cast<const float4v*>(p.ws_o + (base + c) * HD + d) : float4v{0.f, 0.f, 0.f, 0.f};
+            const bool ok = c <= c1;
+            ml[j] = ok ? *reinterpret_cast<const float2*>(p.ws_ml + 2 * (base + c)) : make_float2(-INFINITY, 0.f);
+            ov[j] = ok ? *reinterpret_cast<const float4v*>(p.ws_o + (base + c) * HD + d) : float4v{0.f, 0.f, 0.f, 0.f};
         }
+        float mb = m;
+#pragma unroll
+        for (int j = 0; j < J; ++j) mb = fmaxf(mb, ml[j].x);
+        const float ms = (mb == -INFINITY) ? 0.f : mb;
+        const float f = fast_exp2(m - ms);
+        l *= f;
+        o *= f;
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-            const int c = cb + ph + PH * j;
-            if (c <= c1) acc += ov[j] * s_w[c - c0];
+            const float w = fast_exp2(ml[j].x - ms);
+            l += ml[j].y * w;
+            o += ov[j] * w;
         }
+        m = mb;
     }
-    // the phases in order
-    s_o[tid] = acc;
+    // merge (m, l, o) states: a then b
+    auto merge = [](float& m, float& l, float4v& o, float m2, float l2, const float4v& o2) {
+        const float M = fmaxf(m, m2);
+        const float ms = (M == -INFINITY) ? 0.f : M;
+        const float a = fast_exp2(m - ms), b = fast_exp2(m2 - ms);
+        l = l * a + l2 * b;
+        o = o * a + o2 * b;
+        m = M;
+    };
+    // Exchange with lane ^ off (off = 16 or 32) by permlane swaps (no LDS):
+    // each lane gets the pair (value of the lower lane, value of the upper).
+    auto pair = [](float x, int off) {
+        const auto v = off == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false)
+                                 : __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
+    };
+#pragma unroll
+    for (int off = D4; off < 64; off <<= 1) {
+        // lower phase first; both lanes compute the same merge
+        const float2 mp = pair(m, off), lp = pair(l, off);
+        float4v olo, ohi;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float2 op = pair(o[i], off);
+            olo[i] = op.x;
+            ohi[i] = op.y;
+        }
+        m = mp.x;
+        l = lp.x;
+        o = olo;
+        merge(m, l, o, mp.y, lp.y, ohi);
+    }
+    if (lane < D4) {
+        s_o[wave][lane] = o;
+        s_ml[wave][lane] = make_float2(m, l);
+    }
     __syncthreads();
     if (tid < D4) {
-        const int d = 4 * tid + DW * dq;
-        float4v sum = s_o[tid];
+        float M = s_ml[0][tid].x, L = s_ml[0][tid].y;
+        float4v O = s_o[0][tid];
 #pragma unroll
-        for (int q = 1; q < PH; ++q) sum += s_o[q * D4 + tid];
-        if (p.parts)
-            store_part(p.parts + ((size_t)(s * p.T + t) * p.n_head + h) * (HD + 2), d, M, L, sum);
-        else
-            *reinterpret_cast<float4v*>(p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + d) = sum * (1.f / L);
+        for (int w = 1; w < 4; ++w) merge(M, L, O, s_ml[w][tid].x, s_ml[w][tid].y, s_o[w][tid]);
+        if (p.parts) {
+            store_part(p.parts + ((size_t)(s * p.T + t) * p.n_head + h) * (HD + 2), d, M, L, O);
+        } else {
+            // sink: in the max and the denominator
+            float f = 1.f / L;
+            if (p.sinks) {
+                const float M2 = fmaxf(M, sk);
+                const float ms = (M == -INFINITY) ? 0.f : M;
+                const float wgt = fast_exp2(ms - M2);
+                f = wgt / (L * wgt + fast_exp2(sk - M2));
+            }
+            *reinterpret_cast<float4v*>(p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + d) = O * f;
+        }
     }
 }
 
