@@ -104,11 +104,12 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
     // cache row are then read together (measured ~1 us faster on the 32K
     // gpt-oss layer).  Otherwise 4 waves on one kv head, ~1 wave per SIMD.
     const bool big = pelica::decode_can_use_8_waves(d->hd, rt) && blocks >= 2048 && d->n_kv % 4 == 0;
-    const int nw = big ? 8 : 4;
+    const int big_mode = env_int("PELICA_ATTN_BIG", 0);
+    const int nw = big ? (big_mode == 1 ? 4 : 8) : 4;
     const int wg_heads = big ? 4 : 1;
     // 64-key blocks per wave: enough waves for every SIMD, each streaming
     // several blocks, so the split count (and the combine's work) stays small
-    const int target_waves = std::max(64, env_int("PELICA_ATTN_DECODE_WAVES", big ? 2048 : 1024));
+    const int target_waves = std::max(64, env_int("PELICA_ATTN_DECODE_WAVES", big && big_mode == 0 ? 2048 : 1024));
     int spw = env_int("PELICA_ATTN_SPLIT_BLOCKS", 0);
     if (spw <= 0) spw = (int)std::max<long long>(1, (blocks + target_waves - 1) / target_waves);
     long long split_keys = 64LL * (nw / wg_heads) * spw;

@@ -53,15 +53,15 @@ __device__ __forceinline__ float wave_sum(float x) {
     return x;
 }
 
-#ifndef PELICA_DEXP
-#define PELICA_DEXP 0
-#endif
 #ifndef PELICA_DEPTH64
 #define PELICA_DEPTH64 1
 #endif
 // waves per SIMD the decode kernel is compiled for (register budget 512/n)
 template <int HD, int RT, int NW>
-constexpr int kDecodeOcc = NW == 8 ? 2 : HD == 64 ? (RT <= 2 ? 2 : 1) : 1;
+constexpr int kDecodeOcc = NW == 8 ? 2 : (NW == 4 && HD == 64 && RT <= 2) ? 2 : 1;
+// 4-wave workgroups over 4 kv heads: one wave per SIMD
+template <int HD, int RT, int NW, int H>
+constexpr int kDecodeOccH = (NW == 4 && H == 4) ? 1 : kDecodeOcc<HD, RT, NW>;
 
 // f16 parts the decode kernel splits Q and P into: 2 (hi + lo, ~fp32
 // products) or 1 (f16 only)
@@ -71,8 +71,11 @@ constexpr int kDecodeOcc = NW == 8 ? 2 : HD == 64 ? (RT <= 2 ? 2 : 1) : 1;
 constexpr int kDecodeSplitParts = PELICA_DECODE_PARTS;
 
 // blocks in flight per wave (register budget)
-template <int HD, int RT>
-constexpr int kDecodeDepth = (HD == 64 && RT == 1) ? PELICA_DEPTH64 : 1;
+#ifndef PELICA_DEPTH_H4
+#define PELICA_DEPTH_H4 2
+#endif
+template <int HD, int RT, int NW, int H>
+constexpr int kDecodeDepth = (NW == 4 && H == 4) ? PELICA_DEPTH_H4 : (HD == 64 && RT == 1) ? PELICA_DEPTH64 : 1;
 
 // cache policy bits of the K/V stream loads: nt (streaming, the cache lines
 // are not kept) — each K/V byte is read once
@@ -116,6 +119,18 @@ __device__ __forceinline__ void store_part(float* slot, int d, float m2, float l
     *reinterpret_cast<float2*>(slot + 4 + d) = make_float2(o[2], o[3]);
 }
 
+// Build-time instrumentation (off by default; -DPELICA_DTRACE): lane 0 of
+// every split-kernel wave stores s_memrealtime stamps (100 MHz) at start,
+// first K block staged, V blocks 0 and 1 staged, loop end, merge hand-off
+// and end, plus its XCC/hardware id, into g_dtrace[wave * 8 + k];
+// pelica_attn_debug_trace() copies the array out after a call.
+#ifdef PELICA_DTRACE
+__device__ unsigned long long g_dtrace[1 << 16];
+#define DTRACE(k) do { if (lane == 0) g_dtrace[(((blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * NW + wave) * 8 + (k)] = (k) == 7 ? ((unsigned long long)__builtin_amdgcn_s_getreg(6164) << 32 | __builtin_amdgcn_s_getreg(63492)) : __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define DTRACE(k) do {} while (0)
+#endif
+
 // K blocks in LDS: 16-byte piece p of key row k sits at slot p ^ k_swz(k), so
 // the 16 keys that one ds_read_b128 of the QK^T A operand touches (same
 // piece) fall in distinct banks, and the 8 (hd 64) or 4 (hd 128) keys of one
@@ -138,7 +153,7 @@ __device__ __forceinline__ float ror8(float x) {
 }
 
 template <int HD, int RT, int NW, int H, bool RING, int D, bool PK>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecodeOcc<HD, RT, NW>, 8))) void decode_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecodeOccH<HD, RT, NW, H>, 8))) void decode_kernel(DecodeParams p) {
     static_assert(!PK || RT == 1, "packed hi/lo columns need one row tile");
     constexpr int DS = HD / 32;   // 32-dim k-steps of the QK^T MFMA
     constexpr int DT = HD / 16;   // 16-dim output tiles
@@ -159,6 +174,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
               c16 = lane & 15;
     constexpr int W = NW / H;                   // waves per head
     const int hl = wave % H, wsub = wave / H;   // this wave's head (local) and block phase
+    DTRACE(0);
+    DTRACE(7);
     const int hgroups = p.n_kv / H;
     const int kvh = (blockIdx.y % hgroups) * H + hl, rg = blockIdx.y / hgroups;
     const int s = blockIdx.z;
@@ -208,18 +225,28 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
 
     // D blocks in flight in staging registers
     u32x4 kr[D][VPL], vr[D][VPL];
-    auto issue = [&](u32x4 (&kd)[VPL], u32x4 (&vd)[VPL], int i) {
-        const bool valid = i < nb;
+    auto row_of = [&](int i, int j) -> uint32_t {
         const int kb = blk(i);
+        if (i >= nb) return nrec;
+        if (!RING) return (uint32_t)(kb + KPL * j + vk0) * stride_b;
+        return (uint32_t)((kb + KPL * j + vk0) % p.ring_cap) * stride_b;
+    };
+    // K of a block is requested before its V, so QK^T can start while V is
+    // still arriving
+    auto issue_k = [&](u32x4 (&kd)[VPL], int i) {
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) {
-            uint32_t row;
-            if (!RING) row = valid ? (uint32_t)(kb + KPL * j + vk0) * stride_b : nrec;
-            else row = valid ? (uint32_t)((kb + KPL * j + vk0) % p.ring_cap) * stride_b : nrec;
+        for (int j = 0; j < VPL; ++j)
             kd[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                  rk, row + 16 * (kcol0 ^ k_swz_j<HD>(j)), 0, kKvAux));
-            vd[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, row + vcol, 0, kKvAux));
-        }
+                                                  rk, row_of(i, j) + 16 * (kcol0 ^ k_swz_j<HD>(j)), 0, kKvAux));
+    };
+    auto issue_v = [&](u32x4 (&vd)[VPL], int i) {
+#pragma unroll
+        for (int j = 0; j < VPL; ++j)
+            vd[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, row_of(i, j) + vcol, 0, kKvAux));
+    };
+    auto issue = [&](u32x4 (&kd)[VPL], u32x4 (&vd)[VPL], int i) {
+        issue_k(kd, i);
+        issue_v(vd, i);
     };
 #pragma unroll
     for (int sl = 0; sl < D; ++sl) issue(kr[sl], vr[sl], sl);
@@ -284,14 +311,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
         for (int dt = 0; dt < DT; ++dt) o[dt][rt] = float4v{0.f, 0.f, 0.f, 0.f};
     }
 
-    auto stage = [&](const u32x4 (&ks)[VPL], const u32x4 (&vs)[VPL]) {
-        // the previous block's LDS reads are done (in-order LDS, same wave)
+    // staging registers -> the wave's LDS buffer (the previous block's LDS
+    // reads are done: LDS operations of one wave complete in order)
+    auto stage = [&](char* buf, const u32x4 (&xs)[VPL]) {
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) {
-            *reinterpret_cast<u32x4*>(klds + (j * 64 + lane) * 16) = ks[j];
-            *reinterpret_cast<u32x4*>(vlds + (j * 64 + lane) * 16) = vs[j];
-        }
+        for (int j = 0; j < VPL; ++j) *reinterpret_cast<u32x4*>(buf + (j * 64 + lane) * 16) = xs[j];
         __builtin_amdgcn_wave_barrier();
     };
     // A operand of k-step ds for key tile kt: key 16 kt + c16 (k_swz of it
@@ -301,13 +326,6 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     for (int ds = 0; ds < DS; ++ds) kread[ds] = klds + c16 * (HD * 2) + 16 * ((g + 4 * ds) ^ k_swz<HD>(c16));
     float4v sc[4][RT];
     auto qk = [&]() {
-#if PELICA_DEXP & 1
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt) sc[kt][rt] = float4v{(float)klds[lane + kt], 0.f, 0.f, 0.f};
-        return;
-#endif
         half8 kc[4][DS];
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
@@ -343,10 +361,6 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
             }
     };
     auto softmax_pv = [&](int kb) {
-#if PELICA_DEXP & 2
-        o[0][0] += sc[0][0] + sc[3][RT-1] + float4v{(float)*reinterpret_cast<const _Float16*>(vlds + lane * 16), 0.f, 0.f, 0.f};
-        return;
-#endif
         // mask (blocks at a range boundary only): row r sees keys [lor, posr]
         if (kb < lo_hi || kb + 63 > pos_lo) {
 #pragma unroll
@@ -418,13 +432,18 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
 #pragma unroll
         for (int sl = 0; sl < D; ++sl) {
             if (i + sl < nb) {
-                stage(kr[sl], vr[sl]);
-                issue(kr[sl], vr[sl], i + sl + D);
+                stage(klds, kr[sl]);
+                if (i + sl == 0) DTRACE(1);
+                issue_k(kr[sl], i + sl + D);
                 qk();
+                stage(vlds, vr[sl]);
+                if (i + sl < 2) DTRACE(2 + i + sl);
+                issue_v(vr[sl], i + sl + D);
                 softmax_pv(blk(i + sl));
             }
         }
     }
+    DTRACE(4);
     if (PK) {
         // columns c16 and c16 ^ 8 hold the hi and lo parts of one row
 #pragma unroll
@@ -458,7 +477,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
         if (lane == 0)
             prev = __hip_atomic_fetch_add(&arrivals[hl], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
         prev = __builtin_amdgcn_readfirstlane(prev);
-        if (prev != W - 1) return;
+        if (prev != W - 1) {
+            DTRACE(5);
+            return;
+        }
         // last of the head's waves: merge all W states in wave order
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
@@ -522,6 +544,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
             for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<float4v*>(p.ws_o + idx * HD + 16 * dt + 4 * g) = o[dt][rt];
         }
     }
+    DTRACE(6);
 }
 
 // Combine of the split partials of one query row, in key order, with the
@@ -644,7 +667,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
 template <int HD, int RT, int NW, int H>
 static hipError_t launch_k(const DecodeParams& p, hipStream_t st) {
     dim3 grid(p.n_slot, p.n_kv / p.wg_heads * p.n_rg, p.n_seq);
-    constexpr int D = kDecodeDepth<HD, RT>;
+    constexpr int D = kDecodeDepth<HD, RT, NW, H>;
     {
     ProfScope ps(kProfDecodeSplit, st);
     // up to 8 rows per kv head: hi and lo parts share one MFMA (packed columns)
@@ -679,6 +702,9 @@ hipError_t launch_decode(const DecodeParams& p, int rt, int nw, hipStream_t st) 
         if (nw == 8 && p.wg_heads == 4) {
             if (rt == 1) return launch_k<64, 1, 8, 4>(p, st);
             if (rt == 2) return launch_k<64, 2, 8, 4>(p, st);
+        } else if (nw == 4 && p.wg_heads == 4) {
+            if (rt == 1) return launch_k<64, 1, 4, 4>(p, st);
+            if (rt == 2) return launch_k<64, 2, 4, 4>(p, st);
         } else if (nw == 4 && p.wg_heads == 1) {
             if (rt == 1) return launch_k<64, 1, 4, 1>(p, st);
             if (rt == 2) return launch_k<64, 2, 4, 1>(p, st);
@@ -695,6 +721,12 @@ hipError_t launch_decode(const DecodeParams& p, int rt, int nw, hipStream_t st) 
 __global__ void zero_u32_kernel(unsigned* p, size_t n) {
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0;
 }
+
+#ifdef PELICA_DTRACE
+extern "C" int pelica_attn_debug_trace(void* dst, size_t bytes) {
+    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_dtrace), bytes, 0, hipMemcpyDeviceToHost);
+}
+#endif
 
 hipError_t launch_zero(unsigned* p, size_t n, hipStream_t st) {
     if (!n) return hipSuccess;
