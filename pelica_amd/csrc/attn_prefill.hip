@@ -65,8 +65,22 @@ __device__ __forceinline__ int v_slot(int k, int p) {
     return k * (HD * 2) + ((p ^ ((k & 3) << 1)) << 4);
 }
 
+// waves per SIMD: 2 (64 query rows per wave at hd 64, 32 at hd 128), or 1
+// with 128 rows per wave (the whole register file for one wave)
+template <int HD, int RT>
+constexpr int kPrefillOcc = HD * RT >= 256 ? 1 : 2;
+
+// Build-time instrumentation (off by default; -DPELICA_PTRACE): per wave,
+// shader-clock cycles spent in the tile loop, waiting for tile loads and at
+// the per-chunk barrier, and the number of exact-path chunks, stored in
+// g_ptrace[wave * 4 + k]; pelica_attn_debug_ptrace() copies them out.
+#ifdef PELICA_PTRACE
+__device__ unsigned long long g_ptrace[1 << 17];
+__device__ __forceinline__ unsigned cyc() { return (unsigned)__builtin_amdgcn_s_memtime(); }
+#endif
+
 template <int HD, int RT, bool RING, bool ROUND>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kPrefillOcc<HD, RT>, kPrefillOcc<HD, RT>))) void prefill_kernel(
     PrefillParams p, int n_tb, int TB) {
     constexpr int NW = 4;
     constexpr int KS = HD / 16;                 // 16-dim k-steps of QK^T
@@ -245,6 +259,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
     __syncthreads();
 
+#ifdef PELICA_PTRACE
+    unsigned t_wait = 0, t_bar = 0, n_exact = 0;
+#endif
     float16v s_a[RT], s_b[RT];
     half8 p_a[2][RT], p_b[2][RT];
 #pragma unroll
@@ -308,59 +325,70 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         // The wave's MFMAs (QK^T of c+1, then PV of c-1) interleaved in
         // program order with the softmax of chunk c, so the matrix cores and
         // the vector ALUs work side by side.  The softmax runs as four
-        // stages over all NS scores of the lane (fma, exp2, f16 pack, row-sum
-        // dot), each op far from the one it depends on.
+        // stages (fma, exp2, f16 pack, row-sum dot) skewed by one MFMA slot
+        // each: slot t takes the fmas of scores S(t+1).., the exp2s of
+        // scores S t.., the packs of the pairs exp'd in slot t-1 and the
+        // dots of the pairs packed in slot t-1, so every 32-cycle MFMA has
+        // the same small mix of vector work beside it (S scores per slot).
         constexpr int NM = KS * RT + 2 * DT * RT;  // MFMAs
         constexpr int NS = 16 * RT;                // scores per lane
         constexpr int NP = NS / 2;                 // score pairs
-        constexpr int SKEW = 3;                    // pairs between an exp2 and its pack
-        constexpr int NOPS = NS + NP + SKEW + NP;  // fma, (exp2 pair | pack) slots, dot
+        static_assert(NS % NM == 0, "whole scores per MFMA slot");
+        constexpr int S = NS / NM;
         // y = s*scale - ms in place (ms: the running max, 0 while it is -inf,
         // so the exact path below can recover s*scale = y + ms)
         float ms[RT];
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) ms[rt] = m[rt] == -INFINITY ? 0.f : m[rt];
         float acc[RT][2];
-        float tmp[2 * (SKEW + 1)];
+        float e[NS];
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) acc[rt][0] = acc[rt][1] = 0.f;
-        auto softmax_op = [&](int op) {
-            if (op < NS) {
-                const int rt = op / 16, i = op % 16;
-                s_cur[rt][i] = __builtin_fmaf(s_cur[rt][i], p.qscale, -ms[rt]);
-            } else if (op < NS + NP + SKEW) {
-                const int k = op - NS;  // exp2 of pair k, pack of pair k - SKEW
-                if (k < NP) {
-                    const int rt = k / 8, i = 2 * (k % 8);
-                    tmp[(2 * k) % (2 * (SKEW + 1))] = fast_exp2(s_cur[rt][i]);
-                    tmp[(2 * k + 1) % (2 * (SKEW + 1))] = fast_exp2(s_cur[rt][i + 1]);
-                }
-                if (k >= SKEW) {
-                    const int kk = k - SKEW, rt = kk / 8, i = 2 * (kk % 8);
-                    p_cur[i / 8][rt][i % 8] = (_Float16)tmp[(2 * kk) % (2 * (SKEW + 1))];
-                    p_cur[i / 8][rt][i % 8 + 1] = (_Float16)tmp[(2 * kk + 1) % (2 * (SKEW + 1))];
-                }
-            } else {
-                const int k = op - NS - NP - SKEW, rt = k / 8, i = 2 * (k % 8);
-                acc[rt][k & 1] = __builtin_amdgcn_fdot2(half2{p_cur[i / 8][rt][i % 8], p_cur[i / 8][rt][i % 8 + 1]},
-                                                        one2, acc[rt][k & 1], false);
-            }
+        auto op_fma = [&](int i) {
+            if (i < NS) s_cur[i / 16][i % 16] = __builtin_fmaf(s_cur[i / 16][i % 16], p.qscale, -ms[i / 16]);
         };
+        auto op_exp = [&](int i) {
+            if (i < NS) e[i] = fast_exp2(s_cur[i / 16][i % 16]);
+        };
+        auto op_pack = [&](int k) {
+            const int rt = k / 8, i = 2 * (k % 8);
+            p_cur[i / 8][rt][i % 8] = (_Float16)e[2 * k];
+            p_cur[i / 8][rt][i % 8 + 1] = (_Float16)e[2 * k + 1];
+        };
+        auto op_dot = [&](int k) {
+            const int rt = k / 8, i = 2 * (k % 8);
+            acc[rt][k & 1] = __builtin_amdgcn_fdot2(half2{p_cur[i / 8][rt][i % 8], p_cur[i / 8][rt][i % 8 + 1]}, one2,
+                                                    acc[rt][k & 1], false);
+        };
+        // pairs whose both exp2s are done after slot u: (S (u + 1)) / 2
+        auto packable = [](int u) { return u < 0 ? 0 : (S * (u + 1)) / 2; };
 #pragma unroll
-        for (int i = 0; i < NM; ++i) {
-            const int r = i / RT;  // operand of MFMA i
-            if (i % RT == 0 && r + 2 < NOPD) read_opd(r + 2);
-            if (i < KS * RT) {
-                const int rt = i % RT;
+        for (int j = 0; j < S; ++j) op_fma(j);
+#pragma unroll
+        for (int t = 0; t < NM; ++t) {
+            const int r = t / RT;  // operand of MFMA t
+            if (t % RT == 0 && r + 2 < NOPD) read_opd(r + 2);
+            if (t < KS * RT) {
+                const int rt = t % RT;
                 s_nxt[rt] = mfma32(opd[r], qb[rt][r], s_nxt[rt]);
             } else {
-                const int j = i - KS * RT, w = j / (DT * RT), dt = (j / RT) % DT, rt = j % RT;
+                const int j = t - KS * RT, w = j / (DT * RT), dt = (j / RT) % DT, rt = j % RT;
                 o[dt][rt] = mfma32(opd[r], p_prv[w][rt], o[dt][rt]);
             }
 #pragma unroll
-            for (int op = i * NOPS / NM; op < (i + 1) * NOPS / NM; ++op) softmax_op(op);
+            for (int k = packable(t - 3); k < packable(t - 2); ++k) op_dot(k);
+#pragma unroll
+            for (int k = packable(t - 2); k < packable(t - 1); ++k) op_pack(k);
+#pragma unroll
+            for (int j = 0; j < S; ++j) op_exp(S * t + j);
+#pragma unroll
+            for (int j = 0; j < S; ++j) op_fma(S * (t + 1) + j);
             __builtin_amdgcn_sched_barrier(0);
         }
+#pragma unroll
+        for (int k = packable(NM - 2); k < NP; ++k) op_pack(k);
+#pragma unroll
+        for (int k = packable(NM - 3); k < NP; ++k) op_dot(k);
         float ls[RT];
         bool bad = false;
 #pragma unroll
@@ -397,14 +425,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) l[rt] += ls[rt];
+#ifdef PELICA_PTRACE
+        const unsigned ta = cyc();
+        if ((c & 1) == 0) wait_tiles();
+        const unsigned tb2 = cyc();
+        __syncthreads();
+        t_wait += tb2 - ta;
+        t_bar += cyc() - tb2;
+        n_exact += __builtin_amdgcn_ballot_w64(bad) != 0;
+#else
         if ((c & 1) == 0) wait_tiles();
         __syncthreads();
+#endif
     };
+#ifdef PELICA_PTRACE
+    const unsigned t_start = cyc();
+#endif
     for (int c = 0; c < n_chunks; c += 2) {  // n_chunks is even
         step(c, s_a, s_b, p_b, p_a);
         step(c + 1, s_b, s_a, p_a, p_b);
     }
     pv(n_chunks - 1, p_b);
+#ifdef PELICA_PTRACE
+    if (lane == 0) {
+        const int wid = blockIdx.x * NW + wave;
+        g_ptrace[wid * 4 + 0] = cyc() - t_start;
+        g_ptrace[wid * 4 + 1] = t_wait;
+        g_ptrace[wid * 4 + 2] = t_bar;
+        g_ptrace[wid * 4 + 3] = (unsigned long long)n_exact << 32 | (unsigned)n_chunks;
+    }
+#endif
     }
 
     // O^T lane layout: dim 32 dt + 8 (i / 4) + 4 h2 + i % 4 of row c32
@@ -467,8 +517,17 @@ static hipError_t launch(const PrefillParams& p, hipStream_t st) {
     return hipGetLastError();
 }
 
+#ifdef PELICA_PTRACE
+extern "C" int pelica_attn_debug_ptrace(void* dst, size_t bytes) {
+    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_ptrace), bytes, 0, hipMemcpyDeviceToHost);
+}
+#endif
+
 hipError_t launch_prefill(const PrefillParams& p, hipStream_t st) {
-    if (p.hd == 64) return launch<64, 2>(p, st);
+#ifndef PELICA_PRE_RT64
+#define PELICA_PRE_RT64 2
+#endif
+    if (p.hd == 64) return launch<64, PELICA_PRE_RT64>(p, st);
     if (p.hd == 128) return launch<128, 1>(p, st);
     return hipErrorNotSupported;
 }
