@@ -63,8 +63,15 @@ typedef struct PelicaAttnDesc {
     int32_t ring_cap;  /* 0 = linear cache; else rows of a ring of ring_cap positions
                           (src/oss_batch.rs:205, src/oss.rs:570-572) */
     float scale;       /* logit scale; 0 = 1/sqrt(hd) (src/moe.rs:1263) */
-    uint32_t flags;    /* reserved, must be 0 */
+    uint32_t flags;    /* 0, or PELICA_ATTN_FLAG_SPLIT_ONLY (pelica_attn_decode only) */
 } PelicaAttnDesc;
+
+/* Measurement flag (no counterpart in the reference): pelica_attn_decode
+ * skips the combine of the key splits, leaving the split partials in the
+ * workspace (`out` holds the result only when the call has one split), so a
+ * profiler or a graph of such calls times the split kernel alone.  Rejected
+ * by every other entry point. */
+#define PELICA_ATTN_FLAG_SPLIT_ONLY 1u
 
 /* PELICA_ATTN_VERSION of the loaded library. */
 int pelica_attn_version(void);

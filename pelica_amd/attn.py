@@ -92,6 +92,10 @@ class ProfRecord(ctypes.Structure):
     _fields_ = [("kernel", ctypes.c_int32), ("ms", ctypes.c_float)]
 
 
+# PelicaAttnDesc.flags: decode runs its key-split kernel only (measurement)
+FLAG_SPLIT_ONLY = 1
+
+
 class AttnDesc(ctypes.Structure):
     """``PelicaAttnDesc`` (field meanings in include/pelica_attn.h)."""
 
@@ -187,7 +191,7 @@ def _stream_ptr(stream) -> Optional[int]:
 
 def make_desc(n_head: int, n_kv: int, hd: int, *, n_seq: int = 1, q_tokens: int = 1, kv_len: int,
               seq_kv_len=None, seq_kv_offset=None, kv_row_stride: int = 0, window: int = 0,
-              ring_cap: int = 0, scale: Optional[float] = None) -> AttnDesc:
+              ring_cap: int = 0, scale: Optional[float] = None, flags: int = 0) -> AttnDesc:
     d = AttnDesc()
     d.n_head, d.n_kv, d.hd = n_head, n_kv, hd
     d.n_seq, d.q_tokens, d.kv_len = n_seq, q_tokens, kv_len
@@ -196,7 +200,7 @@ def make_desc(n_head: int, n_kv: int, hd: int, *, n_seq: int = 1, q_tokens: int 
     d.kv_row_stride = kv_row_stride
     d.window, d.ring_cap = window, ring_cap
     d.scale = 0.0 if scale is None else float(scale)
-    d.flags = 0
+    d.flags = flags
     return d
 
 
@@ -227,9 +231,11 @@ def new_workspace(desc: AttnDesc, device="cuda"):
 
 def decode(q, k, v, *, n_kv: int, kv_len: int, sinks=None, window: int = 0, ring_cap: int = 0,
            scale: Optional[float] = None, seq_kv_len=None, seq_kv_offset=None, kv_row_stride: int = 0,
-           out=None, workspace=None, stream=None):
+           out=None, workspace=None, stream=None, split_only: bool = False):
     """Decode attention.  q: f32 [n_seq, q_tokens, n_head, hd] (CUDA);
-    k, v: f16 cache rows (any shape, contiguous); returns f32 like q."""
+    k, v: f16 cache rows (any shape, contiguous); returns f32 like q.
+    split_only (measurement): run the key-split kernel only
+    (PELICA_ATTN_FLAG_SPLIT_ONLY); the result is then not written."""
     import torch
 
     assert q.dtype == torch.float32 and q.dim() == 4 and q.is_contiguous() and q.is_cuda
@@ -238,7 +244,7 @@ def decode(q, k, v, *, n_kv: int, kv_len: int, sinks=None, window: int = 0, ring
     n_seq, T, n_head, hd = q.shape
     desc = make_desc(n_head, n_kv, hd, n_seq=n_seq, q_tokens=T, kv_len=kv_len, seq_kv_len=seq_kv_len,
                      seq_kv_offset=seq_kv_offset, kv_row_stride=kv_row_stride, window=window,
-                     ring_cap=ring_cap, scale=scale)
+                     ring_cap=ring_cap, scale=scale, flags=FLAG_SPLIT_ONLY if split_only else 0)
     lib = load_library()
     need = lib.pelica_attn_workspace_bytes(ctypes.byref(desc))
     if need == 0:

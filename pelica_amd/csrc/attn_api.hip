@@ -38,7 +38,7 @@ int ceil_div(long long a, long long b) { return (int)((a + b - 1) / b); }
 // mla: the latent layout (hd 512, one kv head, no window or ring)
 int check_desc(const PelicaAttnDesc* d, bool mla = false) {
     if (!d) return fail(PELICA_ATTN_EINVAL, "desc is NULL");
-    if (d->flags != 0) return fail(PELICA_ATTN_EINVAL, "flags must be 0 (got %u)", d->flags);
+    if (d->flags & ~PELICA_ATTN_FLAG_SPLIT_ONLY) return fail(PELICA_ATTN_EINVAL, "unknown flags %u", d->flags);
     if (d->n_head <= 0 || d->n_kv <= 0 || d->n_head % d->n_kv)
         return fail(PELICA_ATTN_EINVAL, "n_head %d must be a positive multiple of n_kv %d", d->n_head, d->n_kv);
     if (mla) {
@@ -230,6 +230,7 @@ int run_decode(const PelicaAttnDesc* desc, const float* q, const uint16_t* k, co
     if (rc) return rc;
     if (!q || !k || !v || !(out || parts))
         return fail(PELICA_ATTN_EINVAL, "q, k, v and %s must be non-NULL", parts ? "parts" : "out");
+    if (parts && desc->flags) return fail(PELICA_ATTN_EINVAL, "flags must be 0");
     if (misaligned(q) || misaligned(k) || misaligned(v) || misaligned(out) || misaligned(workspace))
         return fail(PELICA_ATTN_EINVAL, "q, k, v, out and workspace must be 16-byte aligned");
     if (reinterpret_cast<uintptr_t>(parts) % 8) return fail(PELICA_ATTN_EINVAL, "parts must be 8-byte aligned");
@@ -264,6 +265,7 @@ int run_decode(const PelicaAttnDesc* desc, const float* q, const uint16_t* k, co
     p.split_keys = pl.split_keys;
     p.wg_heads = pl.wg_heads;
     p.parts = parts;
+    p.split_only = (desc->flags & PELICA_ATTN_FLAG_SPLIT_ONLY) != 0;
     hipError_t e = pelica::launch_decode(p, pl.rt, pl.nw, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(PELICA_ATTN_EHIP, "decode launch: %s", hipGetErrorString(e));
     return PELICA_ATTN_OK;
@@ -356,6 +358,7 @@ int pelica_attn_prefill(const PelicaAttnDesc* desc, const uint16_t* q, const uin
     g_err[0] = 0;
     int rc = check_desc(desc);
     if (rc) return rc;
+    if (desc->flags) return fail(PELICA_ATTN_EINVAL, "flags must be 0");
     if (!q || !k || !v || !out) return fail(PELICA_ATTN_EINVAL, "q, k, v and out must be non-NULL");
     if (misaligned(q) || misaligned(k) || misaligned(v) || misaligned(out))
         return fail(PELICA_ATTN_EINVAL, "q, k, v and out must be 16-byte aligned");
@@ -397,6 +400,7 @@ int pelica_attn_mla(const PelicaAttnDesc* desc, const float* q, const uint16_t* 
     DecodePlan pl;
     int rc = plan_mla(desc, &pl);
     if (rc) return rc;
+    if (desc->flags) return fail(PELICA_ATTN_EINVAL, "flags must be 0");
     if (!q || !latent || !out) return fail(PELICA_ATTN_EINVAL, "q, latent and out must be non-NULL");
     if (misaligned(q) || misaligned(latent) || misaligned(out) || misaligned(workspace))
         return fail(PELICA_ATTN_EINVAL, "q, latent, out and workspace must be 16-byte aligned");
@@ -438,6 +442,7 @@ int pelica_attn_prefill_round(const PelicaAttnDesc* desc, const uint16_t* q, con
     g_err[0] = 0;
     int rc = check_desc(desc);
     if (rc) return rc;
+    if (desc->flags) return fail(PELICA_ATTN_EINVAL, "flags must be 0");
     if (desc->n_seq != 1 || desc->ring_cap || desc->seq_kv_len)
         return fail(PELICA_ATTN_EINVAL, "rounds take one sequence of a linear cache");
     if (!q || !k_rows || !v_rows || !state) return fail(PELICA_ATTN_EINVAL, "q, k_rows, v_rows and state must be non-NULL");

@@ -681,7 +681,7 @@ static hipError_t launch_k(const DecodeParams& p, hipStream_t st) {
     }
     }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || p.n_slot == 1) return e;
+    if (e != hipSuccess || p.n_slot == 1 || p.split_only) return e;
     return launch_combine(p, st);
 }
 

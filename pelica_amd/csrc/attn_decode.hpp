@@ -30,6 +30,7 @@ struct DecodeParams {
     int split_keys;      // keys per split, a multiple of 64
     int wg_heads;        // kv heads per workgroup: 4 (8-wave workgroups) or 1
     float* parts;        // non-null: write merge_dec partial slots here instead of out
+    bool split_only;     // measurement: skip the combine (partials stay in the workspace)
 };
 
 hipError_t launch_decode(const DecodeParams& p, int rt, int nw, hipStream_t st);

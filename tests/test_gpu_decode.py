@@ -108,6 +108,18 @@ def test_split_count_invariance(monkeypatch):
         assert np.abs(o - outs[0]).max() < 2e-6
 
 
+def test_split_only_leaves_output_alone():
+    # the measurement flag runs the split kernel only: out keeps its contents
+    inp = wl.make_inputs(wl.C3_FULL.scaled(kv_len=8192), "cuda")
+    out = torch.full_like(inp.q, float("nan"))
+    kw = dict(n_kv=8, kv_len=8192, sinks=inp.sinks, out=out)
+    attn.decode(inp.q, inp.k, inp.v, split_only=True, **kw)
+    torch.cuda.synchronize()
+    assert torch.isnan(out).all()
+    attn.decode(inp.q, inp.k, inp.v, **kw)
+    assert_close(as_f64(out), as_f64(oracle_run(inp)), what="after a split-only call")
+
+
 def test_output_is_deterministic():
     inp = wl.make_inputs(wl.C5, "cuda")
     a = gpu_run(inp)

@@ -44,6 +44,24 @@ def test_workspace_sizes():
     assert attn.workspace_bytes(_desc(kv_len=64, n_kv=64, n_head=64)) == 0
 
 
+def test_split_only_flag_is_decode_only():
+    lib = attn.load_library()
+    d = _desc()
+    base = attn.workspace_bytes(d)
+    d.flags = attn.FLAG_SPLIT_ONLY
+    # decode accepts it (same workspace), unknown bits are rejected
+    assert lib.pelica_attn_workspace_bytes(ctypes.byref(d)) == base
+    d.flags = 2
+    assert lib.pelica_attn_workspace_bytes(ctypes.byref(d)) == 0
+    assert "flags" in lib.pelica_attn_last_error().decode()
+    # every other entry point rejects it before touching the GPU
+    d.flags = attn.FLAG_SPLIT_ONLY
+    rc = lib.pelica_attn_prefill(ctypes.byref(d), 16, 16, 16, None, 16, None)
+    assert rc == attn.EINVAL and "flags" in lib.pelica_attn_last_error().decode()
+    rc = lib.pelica_attn_decode_partials(ctypes.byref(d), 16, 16, 16, 16, None, 0, None)
+    assert rc == attn.EINVAL and "flags" in lib.pelica_attn_last_error().decode()
+
+
 @pytest.mark.parametrize("kw,code", [
     (dict(hd=96), attn.EUNSUPPORTED),
     (dict(n_head=60), attn.EINVAL),
