@@ -164,7 +164,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     constexpr int NP = PK ? 1 : kDecodeSplitParts;
     constexpr int BUF = 64 * HD * 2;                   // bytes of one 64-key K or V block
     constexpr int STATE = DT * RT * 64 * 16 + RT * 64 * 8;  // bytes of one wave's (O, m, l)
-    constexpr int WSLOT = 2 * BUF > STATE ? 2 * BUF : STATE;   // LDS per wave: K and V block, then state
+    // LDS per wave: one block buffer that holds the block's K, then (once
+    // QK^T's reads of it are issued: a wave's LDS operations complete in
+    // order) its V; after the last block, the wave's state
+    constexpr int WSLOT = BUF > STATE ? BUF : STATE;
     constexpr int SMEM = WSLOT * NW;
     __shared__ __attribute__((aligned(16))) char smem[SMEM];
     __shared__ unsigned arrivals[H];  // waves of each head done (merge at the end)
@@ -220,7 +223,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     const int nblk_all = (kend - kfirst + 63) / 64;
     const int nb = nblk_all > wsub ? (nblk_all - wsub + W - 1) / W : 0;
     char* klds = smem + wave * WSLOT;
-    char* vlds = klds + BUF;
+    char* vlds = klds;  // V replaces K in the same buffer (see WSLOT)
     auto blk = [&](int i) { return kfirst + 64 * (wsub + W * i); };
 
     // D blocks in flight in staging registers
