@@ -32,6 +32,18 @@ int env_int(const char* name, int dflt) {
 
 bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) != 0; }
 
+// compute units of the current device (queried once per process)
+long long device_cus() {
+    static const long long n = [] {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;  // MI355X
+        return (long long)cus;
+    }();
+    return n;
+}
+
 int ceil_div(long long a, long long b) { return (int)((a + b - 1) / b); }
 
 // Checks shared by decode and prefill.
@@ -105,20 +117,34 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
     // gpt-oss layer).  Otherwise 4 waves on one kv head, ~1 wave per SIMD.
     const bool big = pelica::decode_can_use_8_waves(d->hd, rt) && blocks >= 2048 && d->n_kv % 4 == 0;
     const int big_mode = env_int("PELICA_ATTN_BIG", 0);
-    const int nw = big ? (big_mode == 1 ? 4 : 8) : 4;
     const int wg_heads = big ? 4 : 1;
     // 64-key blocks per wave: enough waves for every SIMD, each streaming
     // several blocks, so the split count (and the combine's work) stays small
     const int target_waves = std::max(64, env_int("PELICA_ATTN_DECODE_WAVES", big && big_mode == 0 ? 2048 : 1024));
     int spw = env_int("PELICA_ATTN_SPLIT_BLOCKS", 0);
     if (spw <= 0) spw = (int)std::max<long long>(1, (blocks + target_waves - 1) / target_waves);
-    long long split_keys = 64LL * (nw / wg_heads) * spw;
-    int n_slot = 0;
-    for (;;) {
-        const int total = ceil_div(d->kv_len, split_keys);
-        n_slot = d->window > 0 ? std::min<int>(total, ceil_div(span, split_keys) + 1) : total;
-        if (n_slot <= pelica::kMaxSlots) break;
-        split_keys *= 2;
+    auto splits = [&](int nw_, long long* sk, int* ns) {
+        long long split_keys = 64LL * (nw_ / wg_heads) * spw;
+        int n_slot = 0;
+        for (;;) {
+            const int total = ceil_div(d->kv_len, split_keys);
+            n_slot = d->window > 0 ? std::min<int>(total, ceil_div(span, split_keys) + 1) : total;
+            if (n_slot <= pelica::kMaxSlots) break;
+            split_keys *= 2;
+        }
+        *sk = split_keys;
+        *ns = n_slot;
+    };
+    int nw = big ? (big_mode == 1 ? 4 : 8) : 4;
+    long long split_keys;
+    int n_slot;
+    splits(nw, &split_keys, &n_slot);
+    // Small head-dim-128 calls: with 4-wave workgroups the grid would not
+    // reach every CU (a CU pulls ~22 GB/s at most here), so split the keys
+    // twice as finely over 2-wave workgroups (OLMoE, Qwen3 decode: ~10 %).
+    if (!big && d->hd == 128 && (long long)n_slot * groups < device_cus()) {
+        nw = 2;
+        splits(nw, &split_keys, &n_slot);
     }
     pl->R = R;
     pl->rt = rt;

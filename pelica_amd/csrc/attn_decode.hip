@@ -716,6 +716,9 @@ hipError_t launch_decode(const DecodeParams& p, int rt, int nw, hipStream_t st) 
     } else if (p.hd == 128 && nw == 4 && p.wg_heads == 1) {
         if (rt == 1) return launch_k<128, 1, 4, 1>(p, st);
         if (rt == 2) return launch_k<128, 2, 4, 1>(p, st);
+    } else if (p.hd == 128 && nw == 2 && p.wg_heads == 1) {
+        if (rt == 1) return launch_k<128, 1, 2, 1>(p, st);
+        if (rt == 2) return launch_k<128, 2, 2, 1>(p, st);
     }
     return hipErrorInvalidValue;
 }
