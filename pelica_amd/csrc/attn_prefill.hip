@@ -24,6 +24,8 @@
 // (src/oss_prefill.rs:408).  Workgroups are ordered so that each XCD works on
 // one kv head (its K/V stays in that XCD's L2) and the longest key ranges
 // start first.
+#include <type_traits>
+
 #include "attn_prefill.hpp"
 #include "attn_prof.hpp"
 
@@ -273,12 +275,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kPrefillOcc
 
     // one chunk: scores of c in s_cur, of c+1 into s_nxt; P of c-1 in
     // p_prv, of c into p_cur
-    auto step = [&](int c, float16v (&s_cur)[RT], float16v (&s_nxt)[RT], const half8 (&p_prv)[2][RT],
+    // PAR = c mod 4 as a compile-time constant: it picks the K/V tile
+    // buffers, so every LDS operand address is a loop-invariant lane offset
+    // plus an immediate.
+    auto step = [&](auto par, int c, float16v (&s_cur)[RT], float16v (&s_nxt)[RT], const half8 (&p_prv)[2][RT],
                     half8 (&p_cur)[2][RT]) {
+        constexpr int PAR = decltype(par)::value;
         // K of tile t+2 and V of tile t+1 at odd chunks c = 2t+1: their
         // buffers' last readers finished at chunk 2t; first readers at 2t+3
         const int t = c >> 1;
-        if (c & 1) {
+        if (PAR & 1) {
             if (t + 2 < n_tiles) load_tile(rk, kbuf + (t & 1) * TILE, t + 2, false);
             if (t + 1 < n_tiles) load_tile(rv, vbuf + ((t + 1) & 1) * TILE, t + 1, true);
         }
@@ -300,9 +306,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kPrefillOcc
         // operands ahead of its first MFMA
         constexpr int NOPD = KS + 2 * DT;
         half8 opd[NOPD];
-        const char* const kt_c = kbuf + (((c + 1) >> 1) & 1) * TILE;
-        const int krow = 32 * ((c + 1) & 1) + c32;
-        const char* const vt_c = vbuf + (((c - 1) >> 1) & 1) * TILE;
+        const char* const kt_c = kbuf + (((PAR + 1) >> 1) & 1) * TILE;
+        const int krow = 32 * ((PAR + 1) & 1) + c32;
+        const char* const vt_c = vbuf + (((PAR + 3) >> 1) & 1) * TILE;  // chunk c-1 (c = 0: the zeroed tile 1)
         auto read_opd = [&](int r) {
             if (r < KS) {
                 opd[r] = *reinterpret_cast<const half8*>(kt_c + k_slot<HD>(krow, 2 * r + h2));
@@ -311,7 +317,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kPrefillOcc
                 // dims 32 dt + 16 (G & 1) + 4 q4; lane 4 r4 + q4 of the group
                 const int w = (r - KS) / DT, dt = (r - KS) % DT;
                 const int G = lane >> 4, r4 = (lane & 15) >> 2, q4 = lane & 3;
-                const int key = 32 * ((c - 1) & 1) + 16 * w + 4 * h2 + r4, dim = 32 * dt + 16 * (G & 1) + 4 * q4;
+                const int key = 32 * ((PAR + 3) & 1) + 16 * w + 4 * h2 + r4, dim = 32 * dt + 16 * (G & 1) + 4 * q4;
                 const _Float16* a0 = reinterpret_cast<const _Float16*>(vt_c + v_slot<HD>(key, dim >> 3) + ((dim & 7) << 1));
                 const _Float16* a1 = reinterpret_cast<const _Float16*>(vt_c + v_slot<HD>(key + 8, dim >> 3) + ((dim & 7) << 1));
                 opd[r] = cat8(lds_read_tr(a0), lds_read_tr(a1));
@@ -427,23 +433,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kPrefillOcc
         for (int rt = 0; rt < RT; ++rt) l[rt] += ls[rt];
 #ifdef PELICA_PTRACE
         const unsigned ta = cyc();
-        if ((c & 1) == 0) wait_tiles();
+        if ((PAR & 1) == 0) wait_tiles();
         const unsigned tb2 = cyc();
         __syncthreads();
         t_wait += tb2 - ta;
         t_bar += cyc() - tb2;
         n_exact += __builtin_amdgcn_ballot_w64(bad) != 0;
 #else
-        if ((c & 1) == 0) wait_tiles();
+        if ((PAR & 1) == 0) wait_tiles();
         __syncthreads();
 #endif
     };
 #ifdef PELICA_PTRACE
     const unsigned t_start = cyc();
 #endif
-    for (int c = 0; c < n_chunks; c += 2) {  // n_chunks is even
-        step(c, s_a, s_b, p_b, p_a);
-        step(c + 1, s_b, s_a, p_a, p_b);
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    using P2 = std::integral_constant<int, 2>;
+    using P3 = std::integral_constant<int, 3>;
+    int c = 0;
+    for (; c + 4 <= n_chunks; c += 4) {
+        step(P0{}, c, s_a, s_b, p_b, p_a);
+        step(P1{}, c + 1, s_b, s_a, p_a, p_b);
+        step(P2{}, c + 2, s_a, s_b, p_b, p_a);
+        step(P3{}, c + 3, s_b, s_a, p_a, p_b);
+    }
+    if (c < n_chunks) {  // n_chunks is even
+        step(P0{}, c, s_a, s_b, p_b, p_a);
+        step(P1{}, c + 1, s_b, s_a, p_a, p_b);
     }
     pv(n_chunks - 1, p_b);
 #ifdef PELICA_PTRACE
