@@ -4,59 +4,85 @@
 // (src/moe_kernels.rs:304-378) and ROPE_KV_T (src/oss_batch.rs:113-170);
 // the f16 rows replace gpt-oss's f32 cache (src/oss.rs:615-616).
 //
-// One wave per (token, head slot): slots [0, n_head) are q heads, then n_kv
-// k heads, then n_kv v heads; lane l holds elements l + 64 i of its head.
-// The norm is a wave reduction; the rotation reads each element's partner
-// through the wave's LDS row.  HBM-bound: every byte is touched once.
+// Head slots [0, n_head) are q heads, then n_kv k heads, then n_kv v heads;
+// a lane holds 4 consecutive elements of its slot (16-byte accesses), a wave
+// 64/(hd/4) slots.  The norm is a reduction over the slot's lanes; the
+// rotation reads each element's partner through the slot's LDS row.
+// HBM-bound: every byte is touched once.
 #include "attn_prof.hpp"
 #include "attn_qkv.hpp"
 
 namespace pelica {
 
-template <int HD>
+// 4 consecutive floats: one 16-byte access (VEC), or four
+template <bool VEC>
+__device__ __forceinline__ float4v load4(const float* p) {
+    if (VEC) return *reinterpret_cast<const float4v*>(p);
+    return float4v{p[0], p[1], p[2], p[3]};
+}
+template <bool VEC>
+__device__ __forceinline__ void store4(float* p, const float4v& x) {
+    if (VEC) {
+        *reinterpret_cast<float4v*>(p) = x;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p[i] = x[i];
+    }
+}
+
+// One lane per 4 consecutive elements of a head: HD/4 lanes per head, 64/(HD/4)
+// heads (slots) per wave.  VEC: 16-byte loads and stores (q/k/v rows and
+// strides 16-byte aligned, cache rows 8-byte aligned).
+template <int HD, bool VEC>
 __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(QkvParams p) {
-    constexpr int EPL = HD / 64;  // elements per lane
-    __shared__ float row[4][HD];
+    constexpr int LPH = HD / 4;     // lanes per head
+    constexpr int HPW = 64 / LPH;   // heads per wave
+    __shared__ float row[4][HPW][HD];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int slot = blockIdx.x * 4 + wave;
+    const int sub = lane / LPH, hl = lane % LPH, e0 = 4 * hl;
+    const int slot = (blockIdx.x * 4 + wave) * HPW + sub;
     const int t = blockIdx.y, s = blockIdx.z;
     const int n_slot = p.n_head + 2 * p.n_kv;
-    if (slot >= n_slot) return;
-    const int kind = slot < p.n_head ? 0 : slot < p.n_head + p.n_kv ? 1 : 2;  // q, k, v
-    const int h = kind == 0 ? slot : kind == 1 ? slot - p.n_head : slot - p.n_head - p.n_kv;
+    const int len = p.seq_len ? p.seq_len[s] : p.kv_len;
+    if (len < p.T || len > p.kv_len) return;  // (attention skips such sequences too)
+    // lanes of slots past the end keep to the wave's lane exchanges with
+    // harmless values and store nothing
+    const bool live = slot < n_slot;
+    const int kind = !live ? 2 : slot < p.n_head ? 0 : slot < p.n_head + p.n_kv ? 1 : 2;  // q, k, v
+    const int h = !live ? 0 : kind == 0 ? slot : kind == 1 ? slot - p.n_head : slot - p.n_head - p.n_kv;
     const size_t tok = (size_t)s * p.T + t;
     const float* src = kind == 0 ? p.q + tok * p.tok_q + (size_t)h * HD
                      : (kind == 1 ? p.k : p.v) + tok * p.tok_kv + (size_t)h * HD;
-    const int len = p.seq_len ? p.seq_len[s] : p.kv_len;
-    if (len < p.T || len > p.kv_len) return;  // (attention skips such sequences too)
     const int pos = len - p.T + t;
 
-    float x[EPL];
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) x[i] = src[lane + 64 * i];
+    float4v x = live ? load4<VEC>(src + e0) : float4v{0.f, 0.f, 0.f, 0.f};
 
+    // per-head RMS norm: the sum of squares over the head's LPH lanes
     const float* w = kind == 0 ? p.q_norm : kind == 1 ? p.k_norm : nullptr;
+    float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
+#pragma unroll
+    for (int off = LPH / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
     if (w) {
-        float ss = 0.f;
-#pragma unroll
-        for (int i = 0; i < EPL; ++i) ss += x[i] * x[i];
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
         const float inv = 1.f / __builtin_sqrtf(ss / (float)HD + p.eps);
+        const float4v wv = load4<false>(w + e0);
 #pragma unroll
-        for (int i = 0; i < EPL; ++i) x[i] = x[i] * inv * w[lane + 64 * i];
+        for (int i = 0; i < 4; ++i) x[i] = x[i] * inv * wv[i];
     }
 
-    if (kind < 2 && p.table) {
-        float* r = row[wave];
-#pragma unroll
-        for (int i = 0; i < EPL; ++i) r[lane + 64 * i] = x[i];
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    // rotary: element e of the first rot pairs with its partner (e +- rot/2,
+    // or e ^ 1 for interleaved pairs), read through the head's LDS row
+    if (p.table && e0 < p.rot) {
+        float* r = row[wave][sub];
+        *reinterpret_cast<float4v*>(r + e0) = x;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    if (kind < 2 && p.table && e0 < p.rot) {
+        const float* r = row[wave][sub];
         const int half = p.rot / 2;
 #pragma unroll
-        for (int i = 0; i < EPL; ++i) {
-            const int e = lane + 64 * i;
+        for (int i = 0; i < 4; ++i) {
+            const int e = e0 + i;
             if (e >= p.rot) continue;
             int j, a, b;
             if (p.neox) {
@@ -85,28 +111,44 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(QkvParams p) {
             x[i] = e == a ? x0 * cs - x1 * sn : x0 * sn + x1 * cs;
         }
     }
+    if (!live) return;
 
     if (kind == 0) {
-        float* dst = p.q + tok * p.tok_q + (size_t)h * HD;
-#pragma unroll
-        for (int i = 0; i < EPL; ++i) dst[lane + 64 * i] = x[i];
+        store4<VEC>(p.q + tok * p.tok_q + (size_t)h * HD + e0, x);
     } else {
         const int64_t base = p.seq_off ? p.seq_off[s] : (int64_t)s * (p.ring_cap ? p.ring_cap : p.kv_len);
         const int64_t rowi = base + (p.ring_cap ? pos % p.ring_cap : pos);
-        uint16_t* dst = (kind == 1 ? p.k_cache : p.v_cache) + rowi * p.row_stride + (int64_t)h * HD;
+        uint16_t* dst = (kind == 1 ? p.k_cache : p.v_cache) + rowi * p.row_stride + (int64_t)h * HD + e0;
+        uint16_t hv[4];
 #pragma unroll
-        for (int i = 0; i < EPL; ++i) dst[lane + 64 * i] = __builtin_bit_cast(uint16_t, (_Float16)x[i]);
+        for (int i = 0; i < 4; ++i) hv[i] = __builtin_bit_cast(uint16_t, (_Float16)x[i]);
+        if (VEC) {
+            *reinterpret_cast<u32x2*>(dst) = u32x2{hv[0] | (uint32_t)hv[1] << 16, hv[2] | (uint32_t)hv[3] << 16};
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dst[i] = hv[i];
+        }
     }
+}
+
+template <int HD>
+static void launch_hd(const QkvParams& p, bool vec, dim3 grid, hipStream_t st) {
+    if (vec) hipLaunchKernelGGL((qkv_rope_cache_kernel<HD, true>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((qkv_rope_cache_kernel<HD, false>), grid, dim3(256), 0, st, p);
 }
 
 hipError_t launch_qkv(const QkvParams& p, hipStream_t st) {
     const int n_slot = p.n_head + 2 * p.n_kv;
-    const dim3 grid((n_slot + 3) / 4, p.T, p.n_seq);
+    const int hpw = 64 / (p.hd / 4);  // heads per wave
+    const dim3 grid((n_slot + 4 * hpw - 1) / (4 * hpw), p.T, p.n_seq);
+    auto al = [](const void* q, int a) { return (reinterpret_cast<uintptr_t>(q) % a) == 0; };
+    const bool vec = al(p.q, 16) && al(p.k, 16) && al(p.v, 16) && p.tok_q % 4 == 0 && p.tok_kv % 4 == 0 &&
+                     al(p.k_cache, 8) && al(p.v_cache, 8) && p.row_stride % 4 == 0;
     ProfScope ps(kProfQkv, st);
     switch (p.hd) {
-        case 64: hipLaunchKernelGGL(qkv_rope_cache_kernel<64>, grid, dim3(256), 0, st, p); break;
-        case 128: hipLaunchKernelGGL(qkv_rope_cache_kernel<128>, grid, dim3(256), 0, st, p); break;
-        case 256: hipLaunchKernelGGL(qkv_rope_cache_kernel<256>, grid, dim3(256), 0, st, p); break;
+        case 64: launch_hd<64>(p, vec, grid, st); break;
+        case 128: launch_hd<128>(p, vec, grid, st); break;
+        case 256: launch_hd<256>(p, vec, grid, st); break;
         default: return hipErrorNotSupported;
     }
     return hipGetLastError();

@@ -109,26 +109,28 @@ def test_no_rope_norm_only():
     _check(*_run_both(q, k, v, n_kv=16, kv_len=50, rows=50, q_norm=w, k_norm=w), "norm only")
 
 
-def test_fused_qkv_rows_with_token_stride():
-    # the engine's activation rows [q heads | k heads | v heads] per token
+@pytest.mark.parametrize("pad", [0, 1])
+def test_fused_qkv_rows_with_token_stride(pad):
+    # the engine's activation rows [q heads | k heads | v heads] per token;
+    # pad 1 makes the token stride odd (no 16-byte row accesses)
     n_head, n_kv, hd, T, L = 64, 8, 64, 3, 900
     qd, kd = n_head * hd, n_kv * hd
     g = torch.Generator(device="cuda").manual_seed(6)
-    act = torch.randn(T, qd + 2 * kd, generator=g, device="cuda")
+    act = torch.randn(T, qd + 2 * kd + pad, generator=g, device="cuda")
     table = torch.from_numpy(orc.rope_table(L, hd)).cuda()
     kc = torch.zeros(L, kd, dtype=torch.float16, device="cuda")
     vc = torch.zeros_like(kc)
     q_view = act[:, :qd]
-    attn.qkv_rope_cache(q_view, act[:, qd:qd + kd], act[:, qd + kd:], kc, vc, n_kv=n_kv, kv_len=L, table=table,
-                        token_stride=qd + 2 * kd, n_seq=1, q_tokens=T, n_head=n_head, hd=hd)
+    attn.qkv_rope_cache(q_view, act[:, qd:qd + kd], act[:, qd + kd:qd + 2 * kd], kc, vc, n_kv=n_kv, kv_len=L,
+                        table=table, token_stride=qd + 2 * kd + pad, n_seq=1, q_tokens=T, n_head=n_head, hd=hd)
     torch.cuda.synchronize()
     a = act.cpu().numpy()
     q = a[:, :qd].reshape(1, T, n_head, hd)
     k = a[:, qd:qd + kd].reshape(1, T, n_kv, hd)
-    v = a[:, qd + kd:].reshape(1, T, n_kv, hd)
+    v = a[:, qd + kd:qd + 2 * kd].reshape(1, T, n_kv, hd)
     # (q was rotated in place: recompute the oracle from the untouched k/v and the original q)
     g2 = torch.Generator(device="cuda").manual_seed(6)
-    q0 = torch.randn(T, qd + 2 * kd, generator=g2, device="cuda").cpu().numpy()[:, :qd].reshape(1, T, n_head, hd)
+    q0 = torch.randn(T, qd + 2 * kd + pad, generator=g2, device="cuda").cpu().numpy()[:, :qd].reshape(1, T, n_head, hd)
     qo, kco, vco = orc.qk_norm_rope_cache(q0, k, v, n_kv=n_kv, kv_len=L, table=table.cpu().numpy())
     assert np.abs(q.astype(np.float64) - qo).max() < 1e-5
     assert np.array_equal(to_np_f16(vc), vco)
