@@ -146,6 +146,14 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
         nw = 2;
         splits(nw, &split_keys, &n_slot);
     }
+    // Window layers: when the keys any row sees fit one workgroup (each wave
+    // <= 2 blocks), one split per kv head — the workgroup merges its waves
+    // and writes the output itself, no combine launch.
+    if (d->window > 0 && !big && (ceil_div(span, 64) + 1) <= 2 * (nw / wg_heads) &&
+        env_int("PELICA_ATTN_SPLIT_BLOCKS", 0) <= 0) {
+        split_keys = ((long long)d->kv_len + 63) / 64 * 64;
+        n_slot = 1;
+    }
     pl->R = R;
     pl->rt = rt;
     pl->n_rg = n_rg;
