@@ -12,24 +12,33 @@
 // HBM once.  Rows sit in the MFMA's 16-wide n dimension.
 //
 // Per 64-key block (software-pipelined one block ahead):
-//   K  global -> registers with 128-bit loads, directly in the A-operand
-//      layout of v_mfma_f32_16x16x32_f16 (lane: key l%16, 8 dims): K never
-//      touches LDS; the next block's K is in flight while this one computes;
-//   S^T[key][row] = K Q^T on MFMA.  Q is split into f16 hi + lo parts (two
-//      MFMAs) so the scores keep ~fp32 accuracy;
+//   K and V global -> staging registers in whole 128-byte lines (streaming
+//      `nt` buffer loads; K's loads are issued before V's), then into the
+//      wave's own LDS buffer (K, and once QK^T's reads of it are issued, V
+//      in the same place: a wave's LDS operations complete in order), with
+//      XOR swizzles that keep the operand reads below bank-conflict free;
+//      the next block's K (V) loads go out as soon as this block's K (V)
+//      is staged;
+//   S^T[key][row] = K Q^T on v_mfma_f32_16x16x32_f16, K read from LDS in
+//      the A-operand layout (ds_read_b128).  Q is split into f16 hi + lo
+//      parts so the scores keep ~fp32 accuracy: with <= 8 rows both parts
+//      share one MFMA (hi in columns 0-7, lo in 8-15, summed across lanes
+//      l, l^8), otherwise they take two;
 //   online softmax in base 2 (log2(e) folded into the query scale); block
-//      max and sums over the four 16-lane groups with permlane swaps;
-//   V  global -> registers (prefetched with K) -> the wave's LDS buffer
-//      (128-bit stores, XOR-swizzled 16-byte pieces), read back with the
-//      transposing ds_read_b64_tr_b16 as the A operand of O^T = V^T P^T; P is
-//      split into f16 hi + lo as the B operand, straight from the score
-//      registers (its key order matches the A operand's).
-// The wave states of each head merge through LDS into one partial (max, sum,
-// O) per row and split; a combine kernel with one 256-thread workgroup per query row
-// merges the splits in key order with the head's sink.  (A one-kernel
-// version, where the last workgroup to arrive combines, was measured slower:
-// every split's arrival is a device-scope atomic on one counter, and those
-// serialize.)  A single split writes the output directly.
+//      max and sums over the four 16-lane groups with permlane swaps; masks
+//      only on blocks that cross a row's key range;
+//   O^T = V^T P^T with V read by the transposing ds_read_b64_tr_b16 as the
+//      A operand and P (hi + lo, packed like Q) as the B operand straight
+//      from the score registers (its key order matches the A operand's).
+// The wave states of each head merge without a workgroup barrier: each wave
+// leaves its state in its LDS buffer and counts itself in on the head's LDS
+// counter, and the last to arrive merges them in wave order into one partial
+// (max, sum, O) per row and split.  A combine kernel (one 256-thread
+// workgroup per query row) merges the splits in key order with the head's
+// sink; a single split writes the output directly.  (In-kernel combines were
+// measured slower on MI355X: the last workgroup alone reading every partial,
+// a grid barrier on one device-scope counter — its atomics serialise — and
+// per-workgroup flags that every workgroup polls.)
 //
 // Reference semantics: src/moe_kernels.rs:482-617 (attn_dec, merge_dec),
 // src/oss_batch.rs:172-251 (ATTN_T: window, ring, sink), :253-425 (attn_s +
