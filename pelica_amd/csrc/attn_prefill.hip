@@ -237,7 +237,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
     // Software pipeline over 32-key chunks: while the softmax of chunk c
     // runs on the vector ALUs, the matrix cores take QK^T of chunk c+1 and
     // PV of chunk c-1.  K tiles and V tiles are double-buffered separately;
-    // one barrier per chunk orders the tile loads against their readers.
+    // one barrier per 64-key tile orders the tile loads against their
+    // readers.
     //
     // Softmax without a per-chunk max: P = 2^(s*scale - m) with the running
     // m; a lane whose chunk sum stays <= 2^14 had no overflow or loss (every
@@ -430,17 +431,26 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
         }
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) l[rt] += ls[rt];
+        // One barrier per tile, after its even chunk c = 2t: (a) the loads
+        // issued at chunk 2t+1 overwrite buffers whose last readers ran at
+        // chunk 2t, and (b) the loads of chunk 2t-1 are first read at chunk
+        // 2t+1, so they must have landed (vmcnt(0)) before it.  Chunk 2t+1
+        // reads only tiles published by this barrier or earlier ones.
+        if ((PAR & 1) == 0) {
 #ifdef PELICA_PTRACE
-        const unsigned ta = cyc();
-        if ((PAR & 1) == 0) wait_tiles();
-        const unsigned tb2 = cyc();
-        __syncthreads();
-        t_wait += tb2 - ta;
-        t_bar += cyc() - tb2;
-        n_exact += __builtin_amdgcn_ballot_w64(bad) != 0;
+            const unsigned ta = cyc();
+            wait_tiles();
+            const unsigned tb2 = cyc();
+            __syncthreads();
+            t_wait += tb2 - ta;
+            t_bar += cyc() - tb2;
 #else
-        if ((PAR & 1) == 0) wait_tiles();
-        __syncthreads();
+            wait_tiles();
+            __syncthreads();
+#endif
+        }
+#ifdef PELICA_PTRACE
+        n_exact += __builtin_amdgcn_ballot_w64(bad) != 0;
 #endif
     };
 #ifdef PELICA_PTRACE
