@@ -371,7 +371,7 @@ def main():
                                         "peak": F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                         "frac": round(pre["kernel_TFLOPs"] / F16_PEAK_TFLOPS, 4),
                                         "traffic": HBM_TRAFFIC_C4,
-                                        "kernel": "prefill_kernel<64,2>: HIP events over graph replays, per launch",
+                                        "kernel": "prefill_kernel<64,2,..,8> (8 waves): HIP events over graph replays, per launch",
                                         "kernel_ms": round(pre["ms"], 5)},
                            "cpu_baseline": cpu_pre}
     print(json.dumps(line), flush=True)
