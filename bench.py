@@ -223,8 +223,9 @@ def bench_qkv(steps, warmup, T=4096, n_head=64, n_kv=8, hd=64):
                 frac_hbm=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, kernel_ms=kt)
 
 
-def cpu_baseline_decode(cfg, reps=5):
-    """The C port of cpu_attn.rs on every host core, full C3 workload."""
+def cpu_baseline_decode(cfg, reps=20):
+    """The C port of cpu_attn.rs on every host core, full C3 workload: one
+    warm-up call, then the median of `reps`."""
     import numpy as np
 
     from oracle import oracle as orc
@@ -248,8 +249,9 @@ def cpu_baseline_decode(cfg, reps=5):
                 ms=sec * 1e3)
 
 
-def cpu_baseline_prefill(cfg, rows=32):
-    """The same port on the last `rows` prompt tokens (the longest key ranges)."""
+def cpu_baseline_prefill(cfg, rows=32, reps=20):
+    """The same port on the last `rows` prompt tokens (the longest key
+    ranges): one warm-up call, then the median of `reps`."""
     import numpy as np
 
     from oracle import oracle as orc
@@ -262,14 +264,21 @@ def cpu_baseline_prefill(cfg, rows=32):
     sinks = inp.sinks.numpy()
     T = cfg.q_tokens
     threads = os.cpu_count() or 1
-    t = time.perf_counter()
-    orc.attention(q, k, v, n_kv=cfg.n_kv, kv_len=cfg.kv_len, sinks=sinks, window=cfg.window, t_begin=T - rows,
-                  t_end=T, threads=threads)
-    sec = time.perf_counter() - t
+    def run():
+        orc.attention(q, k, v, n_kv=cfg.n_kv, kv_len=cfg.kv_len, sinks=sinks, window=cfg.window, t_begin=T - rows,
+                      t_end=T, threads=threads)
+
+    run()
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t)
+    sec = float(np.median(times))
     pairs = sum(min(p + 1, cfg.window) if cfg.window else p + 1 for p in range(T - rows, T))
     flops = 4 * cfg.hd * cfg.n_head * pairs
     return dict(value=flops / sec / 1e12, unit="TFLOP/s", cores=threads, kind="port",
-                sample=f"last {rows} of {T} prompt tokens of {cfg.name}", ms=sec * 1e3)
+                sample=f"last {rows} of {T} prompt tokens of {cfg.name}, median of {reps}", ms=sec * 1e3)
 
 
 def profile_only(args):
