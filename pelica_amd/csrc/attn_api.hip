@@ -94,6 +94,8 @@ float eff_scale(const PelicaAttnDesc* d) { return d->scale > 0.f ? d->scale : 1.
 
 struct DecodePlan {
     int R, rt, n_rg, split_keys, n_slot, wg_heads, nw;
+    bool sk;
+    int sk_grid, sk_minb, sk_restart;
     size_t ctr_bytes, ml_bytes, ws_bytes;
 };
 
@@ -115,7 +117,12 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
     // workgroup (2 waves each), ~2 waves per SIMD — the heads' slices of a
     // cache row are then read together (measured ~1 us faster on the 32K
     // gpt-oss layer).  Otherwise 4 waves on one kv head, ~1 wave per SIMD.
-    const bool big = pelica::decode_can_use_8_waves(d->hd, rt) && blocks >= 2048 && d->n_kv % 4 == 0;
+    // Ragged batches without window or ring go stream-K: a fixed grid shares
+    // the batch's blocks evenly, whatever the spread of the lengths (with
+    // one split grid the longest sequences' workgroups set the time)
+    const bool sk = d->seq_kv_len && d->window == 0 && d->ring_cap == 0 && !(d->hd == 64 && rt == 4) &&
+                    env_int("PELICA_ATTN_STREAMK", 1) != 0 && env_int("PELICA_ATTN_SPLIT_BLOCKS", 0) <= 0;
+    const bool big = !sk && pelica::decode_can_use_8_waves(d->hd, rt) && blocks >= 2048 && d->n_kv % 4 == 0;
     const int big_mode = env_int("PELICA_ATTN_BIG", 0);
     const int wg_heads = big ? 4 : 1;
     // 64-key blocks per wave: enough waves for every SIMD, each streaming
@@ -123,7 +130,7 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
     const int target_waves = std::max(64, env_int("PELICA_ATTN_DECODE_WAVES", big && big_mode == 0 ? 2048 : 1024));
     int spw = env_int("PELICA_ATTN_SPLIT_BLOCKS", 0);
     if (spw <= 0) spw = (int)std::max<long long>(1, (blocks + target_waves - 1) / target_waves);
-    auto splits = [&](int nw_, long long* sk, int* ns) {
+    auto splits = [&](int nw_, long long* keys, int* ns) {
         long long split_keys = 64LL * (nw_ / wg_heads) * spw;
         int n_slot = 0;
         for (;;) {
@@ -132,7 +139,7 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
             if (n_slot <= pelica::kMaxSlots) break;
             split_keys *= 2;
         }
-        *sk = split_keys;
+        *keys = split_keys;
         *ns = n_slot;
     };
     int nw = big ? (big_mode == 1 ? 4 : 8) : 4;
@@ -154,6 +161,29 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
         split_keys = ((long long)d->kv_len + 63) / 64 * 64;
         n_slot = 1;
     }
+    pl->sk = sk;
+    pl->sk_grid = pl->sk_minb = pl->sk_restart = 0;
+    if (sk) {
+        // one 4-wave workgroup per CU (two where two waves per SIMD fit:
+        // head dim 64, one row tile);
+        // ranges of at least minb blocks, and a bound on the pieces of one
+        // segment (a sequence's blocks of one kv head and row group) for
+        // the workspace: its blocks / minb + 1
+        nw = 4;
+        const int per_cu = (d->hd == 64 && rt == 1) ? 2 : 1;
+        pl->sk_grid = (int)(device_cus() * per_cu);
+        // (a piece's start-up is charged as sk_restart blocks: ~15 us of
+        // pipeline refill against ~1.4 us per block of a workgroup's stream)
+        const int restart = std::max(0, env_int("PELICA_ATTN_SK_RESTART", 11));
+        const int maxblk = ceil_div(d->kv_len, 64);
+        const long long bmax = (long long)d->n_seq * d->n_kv * n_rg * (maxblk + restart);
+        int minb = (int)std::min<long long>(64, std::max<long long>(4, bmax / (2LL * pl->sk_grid)));
+        while (ceil_div(maxblk + restart, minb) + 1 > pelica::kMaxSlots) minb *= 2;
+        pl->sk_minb = minb;
+        pl->sk_restart = restart;
+        split_keys = 64;
+        n_slot = std::min(maxblk, ceil_div(maxblk + restart, minb) + 1);
+    }
     pl->R = R;
     pl->rt = rt;
     pl->n_rg = n_rg;
@@ -163,7 +193,8 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
     pl->nw = nw;
     // workspace: (max, sum) pairs, then O rows, 256-byte aligned parts
     const size_t n_part = (size_t)d->n_seq * d->n_kv * R * n_slot;
-    pl->ctr_bytes = 0;
+    // stream-K: the piece count of each segment, then the partials
+    pl->ctr_bytes = sk ? ((size_t)d->n_seq * d->n_kv * n_rg * 4 + 255) & ~(size_t)255 : 0;
     pl->ml_bytes = (n_part * 2 * 4 + 255) & ~(size_t)255;
     pl->ws_bytes = n_slot > 1 ? pl->ctr_bytes + pl->ml_bytes + n_part * d->hd * 4 : 0;
     return PELICA_ATTN_OK;
@@ -300,6 +331,12 @@ int run_decode(const PelicaAttnDesc* desc, const float* q, const uint16_t* k, co
     p.wg_heads = pl.wg_heads;
     p.parts = parts;
     p.split_only = (desc->flags & PELICA_ATTN_FLAG_SPLIT_ONLY) != 0;
+    p.sk = pl.sk;
+    p.sk_grid = pl.sk_grid;
+    p.sk_minb = pl.sk_minb;
+    p.sk_restart = pl.sk_restart;
+    p.rg_rows = 16 * pl.rt;
+    p.ws_np = pl.sk && pl.ws_bytes ? reinterpret_cast<int*>(ws) : nullptr;
     hipError_t e = pelica::launch_decode(p, pl.rt, pl.nw, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(PELICA_ATTN_EHIP, "decode launch: %s", hipGetErrorString(e));
     return PELICA_ATTN_OK;

@@ -40,6 +40,15 @@
 // a grid barrier on one device-scope counter — its atomics serialise — and
 // per-workgroup flags that every workgroup polls.)
 //
+// Ragged batches (no window, no ring) run stream-K instead of one grid of
+// equal key splits: with a split grid the workgroups of the longest
+// sequences set the time (C5: 180 busy workgroups, then a long tail).  A
+// fixed grid of about one workgroup per CU cuts the batch's list of 64-key
+// blocks into equal contiguous ranges; a range may end inside one sequence's
+// segment and continue into the next, and each such piece is a split with
+// its own slot.  Piece starts are charged in the list (SkLayout) because a
+// piece refills the load pipeline.
+//
 // Reference semantics: src/moe_kernels.rs:482-617 (attn_dec, merge_dec),
 // src/oss_batch.rs:172-251 (ATTN_T: window, ring, sink), :253-425 (attn_s +
 // ATTN_M: split partials, sink in max and denominator).
@@ -131,11 +140,17 @@ __device__ __forceinline__ void store_part(float* slot, int d, float m2, float l
 // Build-time instrumentation (off by default; -DPELICA_DTRACE): lane 0 of
 // every split-kernel wave stores s_memrealtime stamps (100 MHz) at start,
 // first K block staged, V blocks 0 and 1 staged, loop end, merge hand-off
-// and end, plus its XCC/hardware id, into g_dtrace[wave * 8 + k];
+// and end, plus its XCC/hardware id, into g_dtrace[wave * 8 + k] (the
+// first 8192 waves of the grid);
 // pelica_attn_debug_trace() copies the array out after a call.
 #ifdef PELICA_DTRACE
 __device__ unsigned long long g_dtrace[1 << 16];
-#define DTRACE(k) do { if (lane == 0) g_dtrace[(((blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * NW + wave) * 8 + (k)] = (k) == 7 ? ((unsigned long long)__builtin_amdgcn_s_getreg(6164) << 32 | __builtin_amdgcn_s_getreg(63492)) : __builtin_amdgcn_s_memrealtime(); } while (0)
+#define DTRACE(k) do { \
+    const size_t i_ = ((((size_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * NW + wave) * 8 + (k); \
+    if (lane == 0 && i_ < (1u << 16)) \
+        g_dtrace[i_] = (k) == 7 ? ((unsigned long long)__builtin_amdgcn_s_getreg(6164) << 32 | __builtin_amdgcn_s_getreg(63492)) \
+                                : __builtin_amdgcn_s_memrealtime(); \
+} while (0)
 #else
 #define DTRACE(k) do {} while (0)
 #endif
@@ -161,8 +176,68 @@ __device__ __forceinline__ float ror8(float x) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, false));
 }
 
-template <int HD, int RT, int NW, int H, bool RING, int D, bool PK>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecodeOccH<HD, RT, NW, H>, 8))) void decode_kernel(DecodeParams p) {
+// Stream-K layout of a ragged batch (no window, no ring): the segments (a
+// sequence's blocks of one row group and kv head), sequence-major, form one
+// list in which segment i takes p.sk_restart positions for its start-up (a
+// piece restarts the load pipeline: measured ~11 blocks' time) and then its
+// 64-key blocks.  The list is cut into g_eff equal contiguous ranges, one
+// per workgroup (at least p.sk_minb positions each), so a workgroup whose
+// range crosses a segment start gets correspondingly fewer blocks.  Each
+// piece of a segment is one split (slot = its index among the segment's
+// pieces).
+struct SkLayout {
+    long long total;  // positions in the list
+    int g_eff, q, rem;  // workgroups used; range of w: q blocks (+1 if w < rem)
+    __device__ long long start(int w) const { return (long long)w * q + min(w, rem); }
+    // the workgroup whose range holds block x
+    __device__ int owner(long long x) const {
+        const long long big = (long long)rem * (q + 1);
+        return x < big ? (int)(x / (q + 1)) : rem + (int)((x - big) / q);
+    }
+};
+
+// a wave-uniform 64-bit value as a scalar
+__device__ __forceinline__ long long uniform64(long long x) {
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)x);
+    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)((unsigned long long)x >> 32));
+    return (long long)((unsigned long long)hi << 32 | lo);
+}
+
+// blocks of sequence s in the stream-K list (0 for a skipped sequence)
+__device__ __forceinline__ int sk_blocks(const DecodeParams& p, int s) {
+    const int len = p.seq_len[s];
+    return (len < p.T || len <= 0) ? 0 : (len + 63) / 64;
+}
+// list positions of one segment of sequence s (start-up + blocks, or 0)
+__device__ __forceinline__ int sk_span(const DecodeParams& p, int s) {
+    const int nb = sk_blocks(p, s);
+    return nb ? nb + p.sk_restart : 0;
+}
+
+// the layout, computed by every lane of the calling wave (uniform result)
+__device__ SkLayout sk_layout(const DecodeParams& p, int gy) {
+    const int lane = threadIdx.x & 63;
+    long long tot = 0;
+    for (int base = 0; base < p.n_seq; base += 64) {
+        long long x = base + lane < p.n_seq ? sk_span(p, base + lane) : 0;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
+        tot += x;
+    }
+    SkLayout L;
+    L.total = uniform64(tot * gy);
+    L.g_eff = __builtin_amdgcn_readfirstlane((int)max(1LL, min((long long)p.sk_grid, L.total / p.sk_minb)));
+    L.q = __builtin_amdgcn_readfirstlane((int)(L.total / L.g_eff));
+    L.rem = __builtin_amdgcn_readfirstlane((int)(L.total % L.g_eff));
+    return L;
+}
+
+template <int HD, int RT, int NW, int H, bool SK>
+constexpr int kDecodeOccK = SK ? ((HD == 64 && RT == 1) ? kDecodeOccH<HD, RT, NW, H> : 1) : kDecodeOccH<HD, RT, NW, H>;
+
+template <int HD, int RT, int NW, int H, bool RING, int D, bool PK, bool SK>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecodeOccK<HD, RT, NW, H, SK>, 8))) void decode_kernel(DecodeParams p) {
+    static_assert(!SK || (H == 1 && !RING), "stream-K: one kv head per workgroup, linear caches");
     static_assert(!PK || RT == 1, "packed hi/lo columns need one row tile");
     constexpr int DS = HD / 32;   // 32-dim k-steps of the QK^T MFMA
     constexpr int DT = HD / 16;   // 16-dim output tiles
@@ -189,18 +264,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     DTRACE(0);
     DTRACE(7);
     const int hgroups = p.n_kv / H;
-    const int kvh = (blockIdx.y % hgroups) * H + hl, rg = blockIdx.y / hgroups;
-    const int s = blockIdx.z;
-    const int len = p.seq_len ? p.seq_len[s] : p.kv_len;
-    if (len < p.T || len <= 0) return;
+
+    // One split: keys [kbeg, kend) of sequence s, row group and kv heads of
+    // by, written to slot `slot` (single: the only split of its rows, which
+    // then writes the output itself).  Uniform over the workgroup.
+    auto split = [&](const int s, const int by, const int len, const int kbeg, const int kend, const int slot,
+                     const bool single) {
+    const int kvh = (by % hgroups) * H + hl, rg = by / hgroups;
     const int64_t row0 = p.seq_off ? p.seq_off[s] : (int64_t)s * (p.ring_cap ? p.ring_cap : p.kv_len);
     const int lo_min = key_range(len, p.T, 0, p.window).lo;
-    const int split0 = lo_min / p.split_keys;
-    const int n_active = min(p.n_slot, (len - 1) / p.split_keys - split0 + 1);
-    const int slot = blockIdx.x;
-    if (slot >= n_active) return;
-    const int kbeg = (split0 + slot) * p.split_keys;
-    const int kend = min(kbeg + p.split_keys, len);
     const int rbase = rg * ROWS;
 
     // ---- K/V stream setup: the first D blocks are requested before
@@ -530,11 +602,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
         if ((PK && c16 >= 8) || r >= p.R) continue;
         const float M = m[rt], L = l[rt];
         const int t = r / p.hpk, h = kvh * p.hpk + r % p.hpk;
-        if (n_active == 1 && p.parts) {
+        if (single && p.parts) {
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt)
                 store_part(p.parts + ((size_t)(s * p.T + t) * p.n_head + h) * (HD + 2), 16 * dt + 4 * g, M, L, o[dt][rt]);
-        } else if (n_active == 1) {
+        } else if (single) {
             // the only split: normalise here, sink in max and denominator
             const float ms = (M == -INFINITY) ? 0.f : M;
             float f;
@@ -557,6 +629,73 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
         }
     }
     DTRACE(6);
+    };  // split
+
+    if (!SK) {
+        const int slot = blockIdx.x, by = blockIdx.y, s = blockIdx.z;
+        const int len = p.seq_len ? p.seq_len[s] : p.kv_len;
+        if (len < p.T || len <= 0) return;
+        const int split0 = key_range(len, p.T, 0, p.window).lo / p.split_keys;
+        const int n_active = min(p.n_slot, (len - 1) / p.split_keys - split0 + 1);
+        if (slot >= n_active) return;
+        const int kbeg = (split0 + slot) * p.split_keys;
+        split(s, by, len, kbeg, min(kbeg + p.split_keys, len), slot, n_active == 1);
+        return;
+    }
+    // stream-K: this workgroup's range of the block list, piece by piece
+    const int gy = hgroups * p.n_rg;
+    const SkLayout L = sk_layout(p, gy);
+    const int w = blockIdx.x;
+    if (w >= L.g_eff || L.total == 0) return;
+    long long cur = L.start(w);
+    const long long end = L.start(w + 1);
+    if (cur >= end) return;
+    // the sequence holding position cur (< total, so some lane of the scan
+    // finds it), and the positions before it
+    int s = 0;
+    long long pre = 0;  // positions before sequence s
+    for (int base = 0; base < p.n_seq; base += 64) {
+        const long long x = base + lane < p.n_seq ? (long long)sk_span(p, base + lane) * gy : 0;
+        long long incl = x;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const long long y = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += y;
+        }
+        const unsigned long long hit = __builtin_amdgcn_ballot_w64(pre + incl > cur);
+        if (hit) {
+            const int j = __builtin_ctzll(hit);
+            s = base + j;
+            pre = uniform64(pre + __shfl(incl - x, j, 64));
+            break;
+        }
+        pre = uniform64(pre + __shfl(incl, 63, 64));
+    }
+    while (cur < end && s < p.n_seq) {
+        const int nb = __builtin_amdgcn_readfirstlane(sk_blocks(p, s));
+        const int span = nb ? nb + p.sk_restart : 0;
+        if (nb == 0 || cur >= pre + (long long)span * gy) {  // past this sequence
+            pre += (long long)span * gy;
+            ++s;
+            continue;
+        }
+        const int len = __builtin_amdgcn_readfirstlane(p.seq_len[s]);
+        const int by = (int)((cur - pre) / span);
+        const long long seg = pre + (long long)by * span + p.sk_restart;  // the segment's first block
+        if (cur < seg) {  // (in the start-up positions)
+            cur = seg;
+            if (cur >= end) break;
+        }
+        const long long pend = min(end, seg + nb);
+        const int slot = w - L.owner(seg);
+        // the segment's first piece records how many pieces it has
+        if (slot == 0 && p.ws_np && tid == 0) p.ws_np[s * gy + by] = L.owner(seg + nb - 1) - w + 1;
+        split(s, by, len, (int)(64 * (cur - seg)), min((int)(64 * (pend - seg)), len), slot,
+              cur == seg && pend == seg + nb);
+        // the next piece reuses the LDS buffers and counters
+        __syncthreads();
+        cur = pend;
+    }
 }
 
 // Combine of the split partials of one query row, in key order, with the
@@ -579,13 +718,23 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
     const int r = blockIdx.x / NQ, dq = blockIdx.x % NQ, kvh = blockIdx.y, s = blockIdx.z;
     const int len = p.seq_len ? p.seq_len[s] : p.kv_len;
     if (len < p.T || len <= 0) return;
-    const int lo_min = key_range(len, p.T, 0, p.window).lo;
-    const int split0 = lo_min / p.split_keys;
-    const int n_active = min(p.n_slot, (len - 1) / p.split_keys - split0 + 1);
-    if (n_active <= 1) return;  // the split kernel wrote the output
     const int t = r / p.hpk, h = kvh * p.hpk + r % p.hpk;
-    const KeyRange krg = key_range(len, p.T, t, p.window);
-    const int c0 = krg.lo / p.split_keys - split0, c1 = min(krg.pos / p.split_keys - split0, n_active - 1);
+    int c0, c1;  // the splits that hold keys of this row
+    if (p.sk) {
+        // stream-K: every piece of the row's segment (rows with no key in a
+        // piece have an empty partial there); the count comes from the split
+        // kernel, and the first pass's loads do not wait for it
+        const int hgroups = p.n_kv / p.wg_heads;
+        c0 = 0;
+        c1 = p.ws_np[s * hgroups * p.n_rg + (r / p.rg_rows) * hgroups + kvh / p.wg_heads] - 1;
+    } else {
+        const int split0 = key_range(len, p.T, 0, p.window).lo / p.split_keys;
+        const int n_active = min(p.n_slot, (len - 1) / p.split_keys - split0 + 1);
+        if (n_active <= 1) return;  // the split kernel wrote the output
+        const KeyRange krg = key_range(len, p.T, t, p.window);
+        c0 = krg.lo / p.split_keys - split0;
+        c1 = min(krg.pos / p.split_keys - split0, n_active - 1);
+    }
     const size_t base = ((size_t)(s * p.n_kv + kvh) * p.R + r) * p.n_slot;
     const int ph = tid / D4, d = 4 * (tid % D4) + DW * dq;
     // the sink logit is requested now, not after the merge
@@ -593,15 +742,25 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
 
     float m = -INFINITY, l = 0.f;
     float4v o = {0.f, 0.f, 0.f, 0.f};
-    for (int cb = c0; cb <= c1; cb += PH * J) {
+    for (int cb = c0;; cb += PH * J) {
         float2 ml[J];
         float4v ov[J];
 #pragma unroll
         for (int j = 0; j < J; ++j) {
             const int c = cb + ph + PH * j;
-            const bool ok = c <= c1;
-            ml[j] = ok ? *reinterpret_cast<const float2*>(p.ws_ml + 2 * (base + c)) : make_float2(-INFINITY, 0.f);
-            ov[j] = ok ? *reinterpret_cast<const float4v*>(p.ws_o + (base + c) * HD + d) : float4v{0.f, 0.f, 0.f, 0.f};
+            // (stream-K, first pass: every slot in the workspace; those past
+            // c1 are dropped below)
+            const bool ld = (p.sk && cb == 0) ? c < p.n_slot : c <= c1;
+            ml[j] = ld ? *reinterpret_cast<const float2*>(p.ws_ml + 2 * (base + c)) : make_float2(-INFINITY, 0.f);
+            ov[j] = ld ? *reinterpret_cast<const float4v*>(p.ws_o + (base + c) * HD + d) : float4v{0.f, 0.f, 0.f, 0.f};
+        }
+        if (p.sk) {
+#pragma unroll
+            for (int j = 0; j < J; ++j)
+                if (cb + ph + PH * j > c1) {
+                    ml[j] = make_float2(-INFINITY, 0.f);
+                    ov[j] = float4v{0.f, 0.f, 0.f, 0.f};
+                }
         }
         float mb = m;
 #pragma unroll
@@ -617,7 +776,9 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
             o += ov[j] * w;
         }
         m = mb;
+        if (cb + PH * J > c1) break;
     }
+    if (p.sk && c1 < 1) return;  // one piece: the split kernel wrote the output
     // merge (m, l, o) states: a then b
     auto merge = [](float& m, float& l, float4v& o, float m2, float l2, const float4v& o2) {
         const float M = fmaxf(m, m2);
@@ -684,12 +845,22 @@ static hipError_t launch_k(const DecodeParams& p, hipStream_t st) {
     ProfScope ps(kProfDecodeSplit, st);
     // up to 8 rows per kv head: hi and lo parts share one MFMA (packed columns)
     const bool pk = RT == 1 && p.R <= 8;
-    if (p.ring_cap) {
-        if (pk) hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, true, D, RT == 1>), grid, dim3(64 * NW), 0, st, p);
-        else hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, true, D, false>), grid, dim3(64 * NW), 0, st, p);
+    if (p.sk) {
+        // (the planner's stream-K shapes: 4 waves on one kv head, up to 32
+        // rows per kv head at head dim 64)
+        if constexpr (H == 1 && NW == 4 && !(HD == 64 && RT == 4)) {
+            if (p.ring_cap || p.window || !p.seq_len) return hipErrorInvalidValue;
+            if (pk) hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, false, D, RT == 1, true>), dim3(p.sk_grid), dim3(64 * NW), 0, st, p);
+            else hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, false, D, false, true>), dim3(p.sk_grid), dim3(64 * NW), 0, st, p);
+        } else {
+            return hipErrorInvalidValue;
+        }
+    } else if (p.ring_cap) {
+        if (pk) hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, true, D, RT == 1, false>), grid, dim3(64 * NW), 0, st, p);
+        else hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, true, D, false, false>), grid, dim3(64 * NW), 0, st, p);
     } else {
-        if (pk) hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, false, D, RT == 1>), grid, dim3(64 * NW), 0, st, p);
-        else hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, false, D, false>), grid, dim3(64 * NW), 0, st, p);
+        if (pk) hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, false, D, RT == 1, false>), grid, dim3(64 * NW), 0, st, p);
+        else hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, false, D, false, false>), grid, dim3(64 * NW), 0, st, p);
     }
     }
     hipError_t e = hipGetLastError();

@@ -31,6 +31,15 @@ struct DecodeParams {
     int wg_heads;        // kv heads per workgroup: 4 (8-wave workgroups) or 1
     float* parts;        // non-null: write merge_dec partial slots here instead of out
     bool split_only;     // measurement: skip the combine (partials stay in the workspace)
+    // stream-K over a ragged batch (no window, no ring; wg_heads 1): a 1-D
+    // grid of sk_grid workgroups shares the batch's 64-key blocks evenly,
+    // each at least sk_minb list positions; n_slot bounds the pieces of a
+    // segment
+    bool sk;
+    int sk_grid, sk_minb;
+    int sk_restart;      // list positions charged at each segment's start (a piece's start-up cost)
+    int* ws_np;          // stream-K: pieces of each (sequence, row group x kv head) segment
+    int rg_rows;         // query rows per row group (16 x row tiles)
 };
 
 hipError_t launch_decode(const DecodeParams& p, int rt, int nw, hipStream_t st);

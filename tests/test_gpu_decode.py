@@ -64,6 +64,30 @@ def test_ragged_batch_with_minimum_lengths():
     check(inp, "ragged minimum lengths")
 
 
+@pytest.mark.parametrize("hd,n_head,n_kv,T,n_seq,kv_len", [
+    (64, 64, 8, 1, 9, 5000),     # gpt-oss batch, one row tile
+    (64, 64, 8, 4, 5, 3000),     # two row tiles
+    (128, 32, 4, 2, 150, 700),   # more sequences than one wave scans at once
+    (128, 16, 16, 1, 40, 2500),  # MHA
+])
+def test_ragged_stream_k(hd, n_head, n_kv, T, n_seq, kv_len):
+    # ragged batches without window or ring share their blocks over a fixed
+    # grid: pieces of a sequence end on arbitrary block boundaries
+    cfg = wl.AttnConfig("sk", "decode", n_head, n_kv, hd, kv_len, q_tokens=T, n_seq=n_seq, ragged=(T, kv_len),
+                        sinks=hd == 64, seed=n_seq)
+    check(wl.make_inputs(cfg, "cuda"), f"stream-K hd{hd} T{T} n_seq{n_seq}")
+
+
+def test_stream_k_matches_grid_splits(monkeypatch):
+    inp = wl.make_inputs(wl.C5.scaled(n_seq=12), "cuda")
+    outs = []
+    for sk in ("0", "1"):
+        monkeypatch.setenv("PELICA_ATTN_STREAMK", sk)
+        check(inp, f"C5 x12, stream-K {sk}")
+        outs.append(as_f64(gpu_run(inp)))
+    assert np.abs(outs[0] - outs[1]).max() < 1e-5
+
+
 def test_batch_without_offsets():
     cfg = wl.AttnConfig("batch", "decode", 16, 4, 64, 700, n_seq=3, seed=21)
     check(wl.make_inputs(cfg, "cuda"), "n_seq 3, default offsets")
