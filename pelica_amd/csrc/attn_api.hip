@@ -123,11 +123,10 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
     const bool sk = d->seq_kv_len && d->window == 0 && d->ring_cap == 0 && !(d->hd == 64 && rt == 4) &&
                     env_int("PELICA_ATTN_STREAMK", 1) != 0 && env_int("PELICA_ATTN_SPLIT_BLOCKS", 0) <= 0;
     const bool big = !sk && pelica::decode_can_use_8_waves(d->hd, rt) && blocks >= 2048 && d->n_kv % 4 == 0;
-    const int big_mode = env_int("PELICA_ATTN_BIG", 0);
     const int wg_heads = big ? 4 : 1;
     // 64-key blocks per wave: enough waves for every SIMD, each streaming
     // several blocks, so the split count (and the combine's work) stays small
-    const int target_waves = std::max(64, env_int("PELICA_ATTN_DECODE_WAVES", big && big_mode == 0 ? 2048 : 1024));
+    const int target_waves = std::max(64, env_int("PELICA_ATTN_DECODE_WAVES", big ? 2048 : 1024));
     int spw = env_int("PELICA_ATTN_SPLIT_BLOCKS", 0);
     if (spw <= 0) spw = (int)std::max<long long>(1, (blocks + target_waves - 1) / target_waves);
     auto splits = [&](int nw_, long long* keys, int* ns) {
@@ -142,7 +141,7 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
         *keys = split_keys;
         *ns = n_slot;
     };
-    int nw = big ? (big_mode == 1 ? 4 : 8) : 4;
+    int nw = big ? 8 : 4;
     long long split_keys;
     int n_slot;
     splits(nw, &split_keys, &n_slot);

@@ -77,9 +77,6 @@ __device__ __forceinline__ float wave_sum(float x) {
 // waves per SIMD the decode kernel is compiled for (register budget 512/n)
 template <int HD, int RT, int NW>
 constexpr int kDecodeOcc = NW == 8 ? 2 : (NW == 4 && HD == 64 && RT <= 2) ? 2 : 1;
-// 4-wave workgroups over 4 kv heads: one wave per SIMD
-template <int HD, int RT, int NW, int H>
-constexpr int kDecodeOccH = (NW == 4 && H == 4) ? 1 : kDecodeOcc<HD, RT, NW>;
 
 // f16 parts the decode kernel splits Q and P into: 2 (hi + lo, ~fp32
 // products) or 1 (f16 only)
@@ -89,11 +86,8 @@ constexpr int kDecodeOccH = (NW == 4 && H == 4) ? 1 : kDecodeOcc<HD, RT, NW>;
 constexpr int kDecodeSplitParts = PELICA_DECODE_PARTS;
 
 // blocks in flight per wave (register budget)
-#ifndef PELICA_DEPTH_H4
-#define PELICA_DEPTH_H4 2
-#endif
-template <int HD, int RT, int NW, int H>
-constexpr int kDecodeDepth = (NW == 4 && H == 4) ? PELICA_DEPTH_H4 : (HD == 64 && RT == 1) ? PELICA_DEPTH64 : 1;
+template <int HD, int RT>
+constexpr int kDecodeDepth = (HD == 64 && RT == 1) ? PELICA_DEPTH64 : 1;
 
 // cache policy bits of the K/V stream loads: nt (streaming, the cache lines
 // are not kept) — each K/V byte is read once
@@ -233,7 +227,7 @@ __device__ SkLayout sk_layout(const DecodeParams& p, int gy) {
 }
 
 template <int HD, int RT, int NW, int H, bool SK>
-constexpr int kDecodeOccK = SK ? ((HD == 64 && RT == 1) ? kDecodeOccH<HD, RT, NW, H> : 1) : kDecodeOccH<HD, RT, NW, H>;
+constexpr int kDecodeOccK = SK ? ((HD == 64 && RT == 1) ? kDecodeOcc<HD, RT, NW> : 1) : kDecodeOcc<HD, RT, NW>;
 
 template <int HD, int RT, int NW, int H, bool RING, int D, bool PK, bool SK>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecodeOccK<HD, RT, NW, H, SK>, 8))) void decode_kernel(DecodeParams p) {
@@ -830,7 +824,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
 template <int HD, int RT, int NW, int H>
 static hipError_t launch_k(const DecodeParams& p, hipStream_t st) {
     dim3 grid(p.n_slot, p.n_kv / p.wg_heads * p.n_rg, p.n_seq);
-    constexpr int D = kDecodeDepth<HD, RT, NW, H>;
+    constexpr int D = kDecodeDepth<HD, RT>;
     {
     ProfScope ps(kProfDecodeSplit, st);
     // up to 8 rows per kv head: hi and lo parts share one MFMA (packed columns)
@@ -875,9 +869,6 @@ hipError_t launch_decode(const DecodeParams& p, int rt, int nw, hipStream_t st) 
         if (nw == 8 && p.wg_heads == 4) {
             if (rt == 1) return launch_k<64, 1, 8, 4>(p, st);
             if (rt == 2) return launch_k<64, 2, 8, 4>(p, st);
-        } else if (nw == 4 && p.wg_heads == 4) {
-            if (rt == 1) return launch_k<64, 1, 4, 4>(p, st);
-            if (rt == 2) return launch_k<64, 2, 4, 4>(p, st);
         } else if (nw == 4 && p.wg_heads == 1) {
             if (rt == 1) return launch_k<64, 1, 4, 1>(p, st);
             if (rt == 2) return launch_k<64, 2, 4, 1>(p, st);
