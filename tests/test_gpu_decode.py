@@ -211,6 +211,37 @@ def test_graph_replays_match_eager():
         _ = (inp.q * 2).sum().item()  # unrelated eager work between replays
 
 
+def test_stream_k_graph_follows_device_lengths():
+    # stream-K computes its layout on the device from seq_kv_len: a graph
+    # recorded once stays right when the lengths change between replays
+    cfg = wl.C5.scaled(n_seq=8, kv_len=6000, ragged=(4, 6000))
+    inp = wl.make_inputs(cfg, "cuda")
+    kw = dict(n_kv=4, kv_len=inp.kv_len, seq_kv_len=inp.seq_len, seq_kv_offset=inp.seq_off)
+    desc = attn.make_desc(32, 4, 128, n_seq=8, q_tokens=4, kv_len=inp.kv_len, seq_kv_len=inp.seq_len,
+                          seq_kv_offset=inp.seq_off)
+    ws = attn.new_workspace(desc)
+    out = torch.empty_like(inp.q)
+    attn.decode(inp.q, inp.k, inp.v, workspace=ws, out=out, **kw)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        attn.decode(inp.q, inp.k, inp.v, workspace=ws, out=out, **kw)
+    gen = torch.Generator().manual_seed(3)
+    orig = inp.seq_len.cpu()
+    for _ in range(3):
+        # new lengths within each sequence's rows (the offsets stay)
+        lens = (4 + (torch.rand(8, generator=gen) * (orig - 3).float()).to(torch.int32)).clamp(max=orig)
+        inp.seq_len.copy_(lens)
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        eager = attn.decode(inp.q, inp.k, inp.v, workspace=attn.new_workspace(desc), **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(got, eager)
+    assert_close(as_f64(got), as_f64(oracle_run(inp)), what="stream-K graph, last lengths")
+
+
 def test_reused_workspace_with_changing_inputs():
     # consecutive calls on one workspace with different queries and caches:
     # the combine must read this call's partials, never an earlier call's
