@@ -698,18 +698,25 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
 // threads; thread (phase, 4-dim chunk) merges the splits c = phase (mod
 // phases) online (running max, rescaled sum), all of its loads in flight
 // at once; the phases of a wave merge through lane exchanges, the four
-// waves through LDS, in a fixed order.
-template <int HD>
+// waves through LDS, in a fixed order.  ROW_WAVES: one wave per row (four
+// rows per workgroup, grid x = R / 4), for rows with few splits (<= 16):
+// no LDS stage, a quarter of the workgroups.
+template <int HD, bool ROW_WAVES>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
+    static_assert(!ROW_WAVES || HD <= 128, "one wave covers the row's dims");
     constexpr int DW = HD < 128 ? HD : 128;  // dims per workgroup (hd 512: four workgroups per row)
     constexpr int NQ = HD / DW;
     constexpr int D4 = DW / 4;
-    constexpr int PH = 256 / D4;        // phases: 16 (hd 64), 8 (hd 128 and 512)
+    // phases: 16 (hd 64), 8 (hd 128 and 512); one wave per row: 4, 2
+    constexpr int PH = (ROW_WAVES ? 64 : 256) / D4;
     constexpr int J = 8;                // splits per thread per pass
     __shared__ float4v s_o[4][D4];
     __shared__ float2 s_ml[4][D4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r = blockIdx.x / NQ, dq = blockIdx.x % NQ, kvh = blockIdx.y, s = blockIdx.z;
+    const int pt = ROW_WAVES ? lane : tid;  // this thread's index within its row
+    const int r = ROW_WAVES ? blockIdx.x * 4 + wave : blockIdx.x / NQ, dq = ROW_WAVES ? 0 : blockIdx.x % NQ;
+    const int kvh = blockIdx.y, s = blockIdx.z;
+    if (ROW_WAVES && r >= p.R) return;
     const int len = p.seq_len ? p.seq_len[s] : p.kv_len;
     if (len < p.T || len <= 0) return;
     const int t = r / p.hpk, h = kvh * p.hpk + r % p.hpk;
@@ -732,9 +739,9 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
         c1 = min(krg.pos / p.split_keys - split0, n_active - 1);
     }
     const size_t base = ((size_t)(s * p.n_kv + kvh) * p.R + r) * p.n_slot;
-    const int ph = tid / D4, d = 4 * (tid % D4) + DW * dq;
+    const int ph = pt / D4, d = 4 * (pt % D4) + DW * dq;
     // the sink logit is requested now, not after the merge
-    const float sk = (p.sinks && !p.parts && tid < D4) ? p.sinks[h] * kLog2e : -INFINITY;
+    const float sk = (p.sinks && !p.parts && pt < D4) ? p.sinks[h] * kLog2e : -INFINITY;
 
     float m = -INFINITY, l = 0.f;
     float4v o = {0.f, 0.f, 0.f, 0.f};
@@ -795,16 +802,23 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
         o = olo;
         merge(m, l, o, mp.y, lp.y, ohi);
     }
-    if (lane < D4) {
-        s_o[wave][lane] = o;
-        s_ml[wave][lane] = make_float2(m, l);
+    if (!ROW_WAVES) {
+        if (lane < D4) {
+            s_o[wave][lane] = o;
+            s_ml[wave][lane] = make_float2(m, l);
+        }
+        __syncthreads();
     }
-    __syncthreads();
-    if (tid < D4) {
-        float M = s_ml[0][tid].x, L = s_ml[0][tid].y;
-        float4v O = s_o[0][tid];
+    if (pt < D4) {
+        float M = m, L = l;
+        float4v O = o;
+        if (!ROW_WAVES) {
+            M = s_ml[0][tid].x;
+            L = s_ml[0][tid].y;
+            O = s_o[0][tid];
 #pragma unroll
-        for (int w = 1; w < 4; ++w) merge(M, L, O, s_ml[w][tid].x, s_ml[w][tid].y, s_o[w][tid]);
+            for (int w = 1; w < 4; ++w) merge(M, L, O, s_ml[w][tid].x, s_ml[w][tid].y, s_o[w][tid]);
+        }
         if (p.parts) {
             store_part(p.parts + ((size_t)(s * p.T + t) * p.n_head + h) * (HD + 2), d, M, L, O);
         } else {
@@ -852,13 +866,23 @@ static hipError_t launch_k(const DecodeParams& p, hipStream_t st) {
     return launch_combine(p, st);
 }
 
+#ifndef PELICA_COMBINE_ROW_WAVE_SLOTS
+#define PELICA_COMBINE_ROW_WAVE_SLOTS 16
+#endif
+
 hipError_t launch_combine(const DecodeParams& p, hipStream_t st) {
     ProfScope ps(kProfDecodeCombine, st);
+    if (p.hd <= 128 && p.n_slot <= PELICA_COMBINE_ROW_WAVE_SLOTS) {
+        const dim3 grid((p.R + 3) / 4, p.n_kv, p.n_seq);
+        if (p.hd == 64) hipLaunchKernelGGL((decode_combine_kernel<64, true>), grid, dim3(256), 0, st, p);
+        else hipLaunchKernelGGL((decode_combine_kernel<128, true>), grid, dim3(256), 0, st, p);
+        return hipGetLastError();
+    }
     const dim3 grid(p.R * (p.hd > 128 ? p.hd / 128 : 1), p.n_kv, p.n_seq);
     switch (p.hd) {
-        case 64: hipLaunchKernelGGL(decode_combine_kernel<64>, grid, dim3(256), 0, st, p); break;
-        case 128: hipLaunchKernelGGL(decode_combine_kernel<128>, grid, dim3(256), 0, st, p); break;
-        case 512: hipLaunchKernelGGL(decode_combine_kernel<512>, grid, dim3(256), 0, st, p); break;
+        case 64: hipLaunchKernelGGL((decode_combine_kernel<64, false>), grid, dim3(256), 0, st, p); break;
+        case 128: hipLaunchKernelGGL((decode_combine_kernel<128, false>), grid, dim3(256), 0, st, p); break;
+        case 512: hipLaunchKernelGGL((decode_combine_kernel<512, false>), grid, dim3(256), 0, st, p); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
