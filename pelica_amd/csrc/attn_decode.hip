@@ -11,14 +11,13 @@
 // tokens (drafts) — ride in the same wave, so every K/V byte is read from
 // HBM once.  Rows sit in the MFMA's 16-wide n dimension.
 //
-// Per 64-key block (software-pipelined one block ahead):
-//   K and V global -> staging registers in whole 128-byte lines (streaming
-//      `nt` buffer loads; K's loads are issued before V's), then into the
-//      wave's own LDS buffer (K, and once QK^T's reads of it are issued, V
-//      in the same place: a wave's LDS operations complete in order), with
-//      XOR swizzles that keep the operand reads below bank-conflict free;
-//      the next block's K (V) loads go out as soon as this block's K (V)
-//      is staged;
+// Per 64-key block (one block in flight per wave):
+//   K and V go from HBM straight into the wave's own K and V LDS buffers
+//      (buffer_load ... lds, streaming `nt`) in whole 128-byte lines; each
+//      lane loads the piece that an XOR swizzle puts in its LDS slot, which
+//      keeps the operand reads below bank-conflict free.  K's loads are
+//      issued before V's; the next block's K (V) loads go out as soon as
+//      this block's K (V) reads are done;
 //   S^T[key][row] = K Q^T on v_mfma_f32_16x16x32_f16, K read from LDS in
 //      the A-operand layout (ds_read_b128).  Q is split into f16 hi + lo
 //      parts so the scores keep ~fp32 accuracy: with <= 8 rows both parts
@@ -53,6 +52,7 @@
 // src/oss_batch.rs:172-251 (ATTN_T: window, ring, sink), :253-425 (attn_s +
 // ATTN_M: split partials, sink in max and denominator).
 #include <algorithm>
+#include <type_traits>
 
 #include "attn_decode.hpp"
 #include "attn_prof.hpp"
@@ -71,9 +71,6 @@ __device__ __forceinline__ float wave_sum(float x) {
     return x;
 }
 
-#ifndef PELICA_DEPTH64
-#define PELICA_DEPTH64 1
-#endif
 // waves per SIMD the decode kernel is compiled for (register budget 512/n)
 template <int HD, int RT, int NW>
 constexpr int kDecodeOcc = NW == 8 ? 2 : (NW == 4 && HD == 64 && RT <= 2) ? 2 : 1;
@@ -84,10 +81,6 @@ constexpr int kDecodeOcc = NW == 8 ? 2 : (NW == 4 && HD == 64 && RT <= 2) ? 2 : 
 #define PELICA_DECODE_PARTS 2
 #endif
 constexpr int kDecodeSplitParts = PELICA_DECODE_PARTS;
-
-// blocks in flight per wave (register budget)
-template <int HD, int RT>
-constexpr int kDecodeDepth = (HD == 64 && RT == 1) ? PELICA_DEPTH64 : 1;
 
 // cache policy bits of the K/V stream loads: nt (streaming, the cache lines
 // are not kept) — each K/V byte is read once
@@ -133,7 +126,7 @@ __device__ __forceinline__ void store_part(float* slot, int d, float m2, float l
 
 // Build-time instrumentation (off by default; -DPELICA_DTRACE): lane 0 of
 // every split-kernel wave stores s_memrealtime stamps (100 MHz) at start,
-// first K block staged, V blocks 0 and 1 staged, loop end, merge hand-off
+// first K block landed, V blocks 0 and 1 landed, loop end, merge hand-off
 // and end, plus its XCC/hardware id, into g_dtrace[wave * 8 + k] (the
 // first 8192 waves of the grid);
 // pelica_attn_debug_trace() copies the array out after a call.
@@ -163,6 +156,24 @@ __device__ __forceinline__ int k_swz(int k) {
 template <int HD>
 __device__ constexpr int k_swz_j(int j) {
     return HD == 64 ? 4 * (j & 1) : (4 * j) & 15;
+}
+
+// 16 bytes per lane from a buffer resource straight into LDS at lds + 16 *
+// lane, with the K/V stream's cache policy
+__device__ __forceinline__ void kv_dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset, char* lds) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, kKvAux);
+}
+
+// s_waitcnt vmcnt(N), the other counters left alone (gfx9 encoding)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+    __asm__ volatile("" ::: "memory");
+}
+// s_waitcnt lgkmcnt(0)
+__device__ __forceinline__ void wait_lgkm0() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __asm__ volatile("" ::: "memory");
 }
 
 // the value of lane l ^ 8 (within each 16-lane row)
@@ -229,7 +240,7 @@ __device__ SkLayout sk_layout(const DecodeParams& p, int gy) {
 template <int HD, int RT, int NW, int H, bool SK>
 constexpr int kDecodeOccK = SK ? ((HD == 64 && RT == 1) ? kDecodeOcc<HD, RT, NW> : 1) : kDecodeOcc<HD, RT, NW>;
 
-template <int HD, int RT, int NW, int H, bool RING, int D, bool PK, bool SK>
+template <int HD, int RT, int NW, int H, bool RING, bool PK, bool SK>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecodeOccK<HD, RT, NW, H, SK>, 8))) void decode_kernel(DecodeParams p) {
     static_assert(!SK || (H == 1 && !RING), "stream-K: one kv head per workgroup, linear caches");
     static_assert(!PK || RT == 1, "packed hi/lo columns need one row tile");
@@ -242,10 +253,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     constexpr int NP = PK ? 1 : kDecodeSplitParts;
     constexpr int BUF = 64 * HD * 2;                   // bytes of one 64-key K or V block
     constexpr int STATE = DT * RT * 64 * 16 + RT * 64 * 8;  // bytes of one wave's (O, m, l)
-    // LDS per wave: one block buffer that holds the block's K, then (once
-    // QK^T's reads of it are issued: a wave's LDS operations complete in
-    // order) its V; after the last block, the wave's state
-    constexpr int WSLOT = BUF > STATE ? BUF : STATE;
+    // LDS per wave: a K and a V block buffer, filled straight from HBM;
+    // after the last block, the wave's state
+    constexpr int WSLOT = 2 * BUF > STATE ? 2 * BUF : STATE;
     constexpr int SMEM = WSLOT * NW;
     __shared__ __attribute__((aligned(16))) char smem[SMEM];
     __shared__ unsigned arrivals[H];  // waves of each head done (merge at the end)
@@ -269,12 +279,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     const int lo_min = key_range(len, p.T, 0, p.window).lo;
     const int rbase = rg * ROWS;
 
-    // ---- K/V stream setup: the first D blocks are requested before
-    //      anything else, so their HBM latency overlaps the query setup ----
+    // ---- K/V stream setup: the first block is requested before anything
+    //      else, so its HBM latency overlaps the query setup ----
     // Buffer resources over this sequence's rows of kv head kvh: 32-bit
     // offsets, and loads at offsets past num_records return 0 without
-    // touching memory — the tail of the last block, and the prefetches
-    // that run past a wave's last block, cost no traffic.
+    // touching memory — the tail of the last block costs no traffic.
     const uint32_t stride_b = (uint32_t)p.row_stride * 2;
     const uint32_t nrec = (RING ? (uint32_t)p.ring_cap : (uint32_t)len) * stride_b;
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
@@ -298,36 +307,30 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     const int nblk_all = (kend - kfirst + 63) / 64;
     const int nb = nblk_all > wsub ? (nblk_all - wsub + W - 1) / W : 0;
     char* klds = smem + wave * WSLOT;
-    char* vlds = klds;  // V replaces K in the same buffer (see WSLOT)
+    char* vlds = klds + BUF;
     auto blk = [&](int i) { return kfirst + 64 * (wsub + W * i); };
 
-    // D blocks in flight in staging registers
-    u32x4 kr[D][VPL], vr[D][VPL];
     auto row_of = [&](int i, int j) -> uint32_t {
         const int kb = blk(i);
         if (i >= nb) return nrec;
         if (!RING) return (uint32_t)(kb + KPL * j + vk0) * stride_b;
         return (uint32_t)((kb + KPL * j + vk0) % p.ring_cap) * stride_b;
     };
-    // K of a block is requested before its V, so QK^T can start while V is
-    // still arriving
-    auto issue_k = [&](u32x4 (&kd)[VPL], int i) {
+    // Load j of a block fills LDS slots j*64 + lane of the wave's buffer
+    // (buffer_load ... lds).  K of a block is requested before its V, so
+    // QK^T can start while V is still arriving.
+    auto issue_k = [&](int i) {
 #pragma unroll
-        for (int j = 0; j < VPL; ++j)
-            kd[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                  rk, row_of(i, j) + 16 * (kcol0 ^ k_swz_j<HD>(j)), 0, kKvAux));
+        for (int j = 0; j < VPL; ++j) kv_dma16(rk, row_of(i, j) + 16 * (kcol0 ^ k_swz_j<HD>(j)), klds + 1024 * j);
     };
-    auto issue_v = [&](u32x4 (&vd)[VPL], int i) {
+    auto issue_v = [&](int i) {
 #pragma unroll
-        for (int j = 0; j < VPL; ++j)
-            vd[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, row_of(i, j) + vcol, 0, kKvAux));
+        for (int j = 0; j < VPL; ++j) kv_dma16(rv, row_of(i, j) + vcol, vlds + 1024 * j);
     };
-    auto issue = [&](u32x4 (&kd)[VPL], u32x4 (&vd)[VPL], int i) {
-        issue_k(kd, i);
-        issue_v(vd, i);
-    };
-#pragma unroll
-    for (int sl = 0; sl < D; ++sl) issue(kr[sl], vr[sl], sl);
+    if (nb > 0) {
+        issue_k(0);
+        issue_v(0);
+    }
 
     // ---- queries of this lane's rows: f16 parts (hi[, lo]) in base 2 ----
     // PK: column c16 < 8 holds the hi part of row c16, column c16 + 8 its lo
@@ -389,14 +392,6 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
         for (int dt = 0; dt < DT; ++dt) o[dt][rt] = float4v{0.f, 0.f, 0.f, 0.f};
     }
 
-    // staging registers -> the wave's LDS buffer (the previous block's LDS
-    // reads are done: LDS operations of one wave complete in order)
-    auto stage = [&](char* buf, const u32x4 (&xs)[VPL]) {
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int j = 0; j < VPL; ++j) *reinterpret_cast<u32x4*>(buf + (j * 64 + lane) * 16) = xs[j];
-        __builtin_amdgcn_wave_barrier();
-    };
     // A operand of k-step ds for key tile kt: key 16 kt + c16 (k_swz of it
     // is k_swz(c16)), logical piece g + 4 ds
     const char* kread[DS];
@@ -503,23 +498,26 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
         }
     };
 
-    // Pipeline D blocks deep.  Every trip issues the block D ahead (beyond
-    // the wave's range such loads are out of bounds and free), so the wait
-    // counts are the same on every trip.
-    for (int i = 0; i < nb; i += D) {
-#pragma unroll
-        for (int sl = 0; sl < D; ++sl) {
-            if (i + sl < nb) {
-                stage(klds, kr[sl]);
-                if (i + sl == 0) DTRACE(1);
-                issue_k(kr[sl], i + sl + D);
-                qk();
-                stage(vlds, vr[sl]);
-                if (i + sl < 2) DTRACE(2 + i + sl);
-                issue_v(vr[sl], i + sl + D);
-                softmax_pv(blk(i + sl));
-            }
+    // One block in flight per wave: K(i), V(i) are outstanding at the top
+    // of trip i (in that order).  A buffer is refilled as soon as its reads
+    // are done (lgkmcnt): K(i+1) after QK^T, V(i+1) after PV.  (Loads past
+    // the wave's last block are not issued, so nothing is pending when the
+    // state reuses the buffers.)
+    for (int i = 0; i < nb; ++i) {
+        wait_vm<VPL>();  // K(i) landed
+        if (i == 0) DTRACE(1);
+        qk();
+        wait_lgkm0();
+        if (i + 1 < nb) {
+            issue_k(i + 1);
+            wait_vm<VPL>();  // V(i) landed
+        } else {
+            wait_vm<0>();
         }
+        if (i < 2) DTRACE(2 + i);
+        softmax_pv(blk(i));
+        wait_lgkm0();
+        if (i + 1 < nb) issue_v(i + 1);
     }
     DTRACE(4);
     if (PK) {
@@ -838,7 +836,6 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
 template <int HD, int RT, int NW, int H>
 static hipError_t launch_k(const DecodeParams& p, hipStream_t st) {
     dim3 grid(p.n_slot, p.n_kv / p.wg_heads * p.n_rg, p.n_seq);
-    constexpr int D = kDecodeDepth<HD, RT>;
     {
     ProfScope ps(kProfDecodeSplit, st);
     // up to 8 rows per kv head: hi and lo parts share one MFMA (packed columns)
@@ -848,17 +845,17 @@ static hipError_t launch_k(const DecodeParams& p, hipStream_t st) {
         // rows per kv head at head dim 64)
         if constexpr (H == 1 && NW == 4 && !(HD == 64 && RT == 4)) {
             if (p.ring_cap || p.window || !p.seq_len) return hipErrorInvalidValue;
-            if (pk) hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, false, D, RT == 1, true>), dim3(p.sk_grid), dim3(64 * NW), 0, st, p);
-            else hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, false, D, false, true>), dim3(p.sk_grid), dim3(64 * NW), 0, st, p);
+            if (pk) hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, false, RT == 1, true>), dim3(p.sk_grid), dim3(64 * NW), 0, st, p);
+            else hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, false, false, true>), dim3(p.sk_grid), dim3(64 * NW), 0, st, p);
         } else {
             return hipErrorInvalidValue;
         }
     } else if (p.ring_cap) {
-        if (pk) hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, true, D, RT == 1, false>), grid, dim3(64 * NW), 0, st, p);
-        else hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, true, D, false, false>), grid, dim3(64 * NW), 0, st, p);
+        if (pk) hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, true, RT == 1, false>), grid, dim3(64 * NW), 0, st, p);
+        else hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, true, false, false>), grid, dim3(64 * NW), 0, st, p);
     } else {
-        if (pk) hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, false, D, RT == 1, false>), grid, dim3(64 * NW), 0, st, p);
-        else hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, false, D, false, false>), grid, dim3(64 * NW), 0, st, p);
+        if (pk) hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, false, RT == 1, false>), grid, dim3(64 * NW), 0, st, p);
+        else hipLaunchKernelGGL((decode_kernel<HD, RT, NW, H, false, false, false>), grid, dim3(64 * NW), 0, st, p);
     }
     }
     hipError_t e = hipGetLastError();
