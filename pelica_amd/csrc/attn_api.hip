@@ -172,8 +172,9 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
         const int per_cu = (d->hd == 64 && rt == 1) ? 2 : 1;
         pl->sk_grid = (int)(device_cus() * per_cu);
         // (a piece's start-up is charged as sk_restart blocks: ~15 us of
-        // pipeline refill against ~1.4 us per block of a workgroup's stream)
-        const int restart = std::max(0, env_int("PELICA_ATTN_SK_RESTART", 11));
+        // pipeline refill against ~1.4 us per block of a workgroup's
+        // stream; 8 measured best, 6-14 within 1.5 %)
+        const int restart = std::max(0, env_int("PELICA_ATTN_SK_RESTART", 8));
         const int maxblk = ceil_div(d->kv_len, 64);
         const long long bmax = (long long)d->n_seq * d->n_kv * n_rg * (maxblk + restart);
         int minb = (int)std::min<long long>(64, std::max<long long>(4, bmax / (2LL * pl->sk_grid)));

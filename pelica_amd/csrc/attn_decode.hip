@@ -184,7 +184,7 @@ __device__ __forceinline__ float ror8(float x) {
 // Stream-K layout of a ragged batch (no window, no ring): the segments (a
 // sequence's blocks of one row group and kv head), sequence-major, form one
 // list in which segment i takes p.sk_restart positions for its start-up (a
-// piece restarts the load pipeline: measured ~11 blocks' time) and then its
+// piece restarts the load pipeline: ~8-11 blocks' time) and then its
 // 64-key blocks.  The list is cut into g_eff equal contiguous ranges, one
 // per workgroup (at least p.sk_minb positions each), so a workgroup whose
 // range crosses a segment start gets correspondingly fewer blocks.  Each
