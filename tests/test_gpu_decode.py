@@ -78,6 +78,15 @@ def test_ragged_stream_k(hd, n_head, n_kv, T, n_seq, kv_len):
     check(wl.make_inputs(cfg, "cuda"), f"stream-K hd{hd} T{T} n_seq{n_seq}")
 
 
+@pytest.mark.parametrize("window,T", [(128, 1), (300, 4)])
+def test_ragged_batch_with_window(window, T):
+    # ragged batches of a window layer stay on the split grid (stream-K
+    # takes no window); some sequences are shorter than the window
+    cfg = wl.AttnConfig("ragged-win", "decode", 64, 8, 64, 4000, q_tokens=T, n_seq=7, ragged=(T, 4000), window=window,
+                        sinks=True, seed=window + T)
+    check(wl.make_inputs(cfg, "cuda"), f"ragged window {window} T{T}")
+
+
 def test_stream_k_matches_grid_splits(monkeypatch):
     inp = wl.make_inputs(wl.C5.scaled(n_seq=12), "cuda")
     outs = []
