@@ -33,15 +33,17 @@
 // leaves its state in its LDS buffer and counts itself in on the head's LDS
 // counter, and the last to arrive merges them in wave order into one partial
 // (max, sum, O) per row and split.  A combine kernel (one 256-thread
-// workgroup per query row) merges the splits in key order with the head's
-// sink; a single split writes the output directly.  (In-kernel combines were
+// workgroup per query row, or one wave per row when rows have few splits)
+// merges the splits in key order with the head's sink; a single split
+// writes the output directly.  (In-kernel combines were
 // measured slower on MI355X: the last workgroup alone reading every partial,
 // a grid barrier on one device-scope counter — its atomics serialise — and
 // per-workgroup flags that every workgroup polls.)
 //
 // Ragged batches (no window, no ring) run stream-K instead of one grid of
 // equal key splits: with a split grid the workgroups of the longest
-// sequences set the time (C5: 180 busy workgroups, then a long tail).  A
+// sequences set the time (32 sequences of 512-16K keys: 180 busy
+// workgroups, then a long tail).  A
 // fixed grid of about one workgroup per CU cuts the batch's list of 64-key
 // blocks into equal contiguous ranges; a range may end inside one sequence's
 // segment and continue into the next, and each such piece is a split with
@@ -52,7 +54,6 @@
 // src/oss_batch.rs:172-251 (ATTN_T: window, ring, sink), :253-425 (attn_s +
 // ATTN_M: split partials, sink in max and denominator).
 #include <algorithm>
-#include <type_traits>
 
 #include "attn_decode.hpp"
 #include "attn_prof.hpp"
@@ -723,7 +724,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
         // stream-K: every piece of the row's segment (rows with no key in a
         // piece have an empty partial there); the split kernel records the
         // count.  (Loading every workspace slot before the count arrives was
-        // measured slower: 12.6 vs 11.7 us on C5.)
+        // measured slower: 12.6 vs 11.7 us on a 32-sequence draft batch.)
         const int hgroups = p.n_kv / p.wg_heads;
         c0 = 0;
         c1 = p.ws_np[s * hgroups * p.n_rg + (r / p.rg_rows) * hgroups + kvh / p.wg_heads] - 1;

@@ -375,8 +375,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
             const int r = t / RT;  // operand of MFMA t
             if (t % RT == 0 && r + 2 < NOPD) read_opd(r + 2);
             // 8-wave workgroups: the wave about to issue its MFMA takes
-            // issue priority over its SIMD partner's vector work (C4 full
-            // ~1.7 % faster; 4-wave window launches ~3 % slower with it)
+            // issue priority over its SIMD partner's vector work (the
+            // 4096-token gpt-oss causal prefill ~1.7 % faster; 4-wave
+            // window launches ~3 % slower with it)
             if (NW == 8) __builtin_amdgcn_s_setprio(3);
             if (t < KS * RT) {
                 const int rt = t % RT;
@@ -548,9 +549,9 @@ static hipError_t launch_nw(const PrefillParams& p, hipStream_t st) {
 }
 
 // Workgroup size: 8 waves (2 per SIMD from one workgroup: each K/V tile in
-// LDS serves twice the rows; C4 full causal ~2 % faster) unless a short
-// window makes the larger token block mostly masked (window 128: 4 waves,
-// 25 % faster than 8).
+// LDS serves twice the rows; the 4096-token gpt-oss causal prefill ~2 %
+// faster) unless a short window makes the larger token block mostly masked
+// (window 128: 4 waves, 25 % faster than 8).
 template <int HD, int RT>
 static hipError_t launch(const PrefillParams& p, hipStream_t st) {
     if (p.window > 0 && p.window <= 1024) return launch_nw<HD, RT, 4>(p, st);
