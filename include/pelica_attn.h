@@ -54,7 +54,8 @@ typedef struct PelicaAttnDesc {
     int32_t hd;        /* dims per head: 64 or 128 */
     int32_t n_seq;     /* sequences in the batch (>= 1) */
     int32_t q_tokens;  /* query tokens per sequence: 1 decode, <= 8 drafts, T prompt */
-    int32_t kv_len;    /* keys per sequence; with seq_kv_len set, an upper bound */
+    int32_t kv_len;    /* keys per sequence; with seq_kv_len set, an upper bound
+                          (larger seq_kv_len entries are clipped to it) */
     const int32_t* seq_kv_len;    /* device [n_seq] keys per sequence, or NULL */
     const int64_t* seq_kv_offset; /* device [n_seq] first cache row, or NULL:
                                      sequence s then starts at row s * (ring_cap ? ring_cap : kv_len) */
@@ -78,6 +79,13 @@ int pelica_attn_version(void);
 
 /* Message of the calling thread's last failed call ("" if none). */
 const char* pelica_attn_last_error(void);
+
+/* Measurement and test switch (no counterpart in the reference): the
+ * planner's PELICA_ATTN_* tuning variables are read from the environment
+ * once, at the first call that plans a pass; this re-reads them.  Plans and
+ * workspace sizes may change with it: size workspaces again afterwards.
+ * Not safe while another thread plans a call. */
+int pelica_attn_reload_tuning(void);
 
 /* Bytes of device workspace pelica_attn_decode needs for this descriptor
  * (split-K partials).  0 on an invalid descriptor (see last_error) or when
@@ -158,12 +166,25 @@ int pelica_attn_prefill_round(const PelicaAttnDesc* desc, const uint16_t* q, con
 /* Combine n_parts partial slots of one decode token (parts[(c*n_head+h)*(hd+2)],
  * natural-log max) in slot order, with optional sinks, into out[n_head][hd].
  * Slots whose max is -3e38 (or -inf) carry no weight, as the reference's
- * empty slots do.  Replaces merge_dec (src/moe_kernels.rs:585-617) and
- * ATTN_M's combine (src/oss_batch.rs:395-425); it is how partials from the
- * CPU tier (cpu_attn::chunk, src/moe.rs:1686-1729) join the GPU's. */
+ * empty slots do.  hd even, <= 1024; parts and out 8-byte aligned.
+ * Replaces merge_dec (src/moe_kernels.rs:585-617) and ATTN_M's combine
+ * (src/oss_batch.rs:395-425); it is how partials from the CPU tier
+ * (cpu_attn::chunk, src/moe.rs:1686-1729) join the GPU's.  Same as
+ * pelica_attn_partials_merge_batch with n_tokens = 1. */
 int pelica_attn_partials_merge(int32_t n_head, int32_t hd, int32_t n_parts,
                                const float* parts, const float* sinks, float* out,
                                void* stream);
+
+/* The same merge for n_tokens query tokens at once (e.g. n_seq * q_tokens
+ * rows of a draft-verify pass): slot c of token t, head h at
+ * parts[((c*n_tokens + t)*n_head + h)*(hd+2)], output out[t][n_head][hd]
+ * (so the slots that pelica_attn_decode_partials writes for a whole pass are
+ * one slot c here).  Each slot's weight is computed once per (token, head).
+ * Replaces ATTN_M over its (n_head, TMAX) grid (src/oss_batch.rs:395-425)
+ * and merge_dec_fast (src/moe_kernels.rs:750-808). */
+int pelica_attn_partials_merge_batch(int32_t n_tokens, int32_t n_head, int32_t hd, int32_t n_parts,
+                                     const float* parts, const float* sinks, float* out,
+                                     void* stream);
 
 /* ---- the step before attention ----------------------------------------- */
 

@@ -32,6 +32,7 @@ EWORKSPACE = -4
 EXPORTS = (
     "pelica_attn_version",
     "pelica_attn_last_error",
+    "pelica_attn_reload_tuning",
     "pelica_attn_workspace_bytes",
     "pelica_attn_workspace_init",
     "pelica_attn_decode",
@@ -41,6 +42,7 @@ EXPORTS = (
     "pelica_attn_prefill",
     "pelica_attn_prefill_round",
     "pelica_attn_partials_merge",
+    "pelica_attn_partials_merge_batch",
     "pelica_attn_qkv_rope_cache",
     "pelica_attn_prof_enable",
     "pelica_attn_prof_read",
@@ -142,6 +144,8 @@ def load_library() -> ctypes.CDLL:
     lib.pelica_attn_version.argtypes = []
     lib.pelica_attn_last_error.restype = ctypes.c_char_p
     lib.pelica_attn_last_error.argtypes = []
+    lib.pelica_attn_reload_tuning.restype = ctypes.c_int
+    lib.pelica_attn_reload_tuning.argtypes = []
     lib.pelica_attn_workspace_bytes.restype = sz
     lib.pelica_attn_workspace_bytes.argtypes = [dp]
     lib.pelica_attn_workspace_init.restype = ctypes.c_int
@@ -163,6 +167,8 @@ def load_library() -> ctypes.CDLL:
                                                ctypes.c_float, vp, vp, vp]
     lib.pelica_attn_partials_merge.restype = ctypes.c_int
     lib.pelica_attn_partials_merge.argtypes = [i32, i32, i32, vp, vp, vp, vp]
+    lib.pelica_attn_partials_merge_batch.restype = ctypes.c_int
+    lib.pelica_attn_partials_merge_batch.argtypes = [i32, i32, i32, i32, vp, vp, vp, vp]
     lib.pelica_attn_prof_enable.restype = ctypes.c_int
     lib.pelica_attn_prof_enable.argtypes = [ctypes.c_int]
     lib.pelica_attn_prof_read.restype = ctypes.c_int
@@ -415,6 +421,32 @@ def partials_merge(parts, *, n_head: int, hd: int, sinks=None, out=None, stream=
     _check(lib.pelica_attn_partials_merge(n_head, hd, n_parts, _ptr(parts), _ptr(sinks), _ptr(out),
                                           _stream_ptr(stream)))
     return out
+
+
+def partials_merge_batch(parts, *, sinks=None, out=None, stream=None):
+    """Combine partial slots [n_parts, n_tokens, n_head, hd + 2] per (token,
+    head) in slot order with optional sinks into f32 [n_tokens, n_head, hd]
+    (ATTN_M over all the pass's tokens)."""
+    import torch
+
+    assert parts.dtype == torch.float32 and parts.is_cuda and parts.is_contiguous() and parts.dim() == 4
+    n_parts, n_tok, n_head, hp = parts.shape
+    hd = hp - 2
+    if out is None:
+        out = torch.empty(n_tok, n_head, hd, dtype=torch.float32, device=parts.device)
+    assert out.dtype == torch.float32 and out.is_contiguous() and out.numel() == n_tok * n_head * hd
+    if sinks is not None:
+        assert sinks.dtype == torch.float32 and sinks.is_cuda and sinks.numel() == n_head
+    lib = load_library()
+    _check(lib.pelica_attn_partials_merge_batch(n_tok, n_head, hd, n_parts, _ptr(parts), _ptr(sinks), _ptr(out),
+                                                _stream_ptr(stream)))
+    return out
+
+
+def reload_tuning() -> None:
+    """Re-read the planner's PELICA_ATTN_* environment switches (they are
+    otherwise read once per process)."""
+    _check(load_library().pelica_attn_reload_tuning())
 
 
 def default_scale(hd: int) -> float:

@@ -8,6 +8,7 @@
 
 #include "../../include/pelica_attn.h"
 #include "attn_decode.hpp"
+#include "attn_merge.hpp"
 #include "attn_prefill.hpp"
 #include "attn_qkv.hpp"
 #include "attn_prof.hpp"
@@ -29,6 +30,34 @@ int env_int(const char* name, int dflt) {
     if (!s || !*s) return dflt;
     return atoi(s);
 }
+
+// The planner's tuning switches, read from the environment once per process
+// (at the first call that plans a decode or MLA pass): the plan, and with it
+// the workspace size, cannot change between calls.  0 = unset.
+struct Tuning {
+    bool streamk;       // PELICA_ATTN_STREAMK (default 1)
+    int split_blocks;   // PELICA_ATTN_SPLIT_BLOCKS (64-key blocks per wave; > 0 also turns stream-K off)
+    int decode_waves;   // PELICA_ATTN_DECODE_WAVES (target waves of a split grid)
+    int sk_restart;     // PELICA_ATTN_SK_RESTART (positions charged per stream-K piece start)
+    int mla_workgroups; // PELICA_ATTN_MLA_WORKGROUPS
+};
+
+Tuning read_tuning() {
+    Tuning x;
+    x.streamk = env_int("PELICA_ATTN_STREAMK", 1) != 0;
+    x.split_blocks = std::max(0, env_int("PELICA_ATTN_SPLIT_BLOCKS", 0));
+    x.decode_waves = std::max(0, env_int("PELICA_ATTN_DECODE_WAVES", 0));
+    x.sk_restart = env_int("PELICA_ATTN_SK_RESTART", -1);
+    x.mla_workgroups = std::max(0, env_int("PELICA_ATTN_MLA_WORKGROUPS", 0));
+    return x;
+}
+
+Tuning& tuning_slot() {
+    static Tuning t = read_tuning();
+    return t;
+}
+
+const Tuning& tuning() { return tuning_slot(); }
 
 bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) != 0; }
 
@@ -102,6 +131,7 @@ struct DecodePlan {
 int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
     int rc = check_desc(d);
     if (rc) return rc;
+    const Tuning& tn = tuning();
     const int hpk = d->n_head / d->n_kv;
     const int R = d->q_tokens * hpk;
     int rt;
@@ -121,13 +151,13 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
     // the batch's blocks evenly, whatever the spread of the lengths (with
     // one split grid the longest sequences' workgroups set the time)
     const bool sk = d->seq_kv_len && d->window == 0 && d->ring_cap == 0 && !(d->hd == 64 && rt == 4) &&
-                    env_int("PELICA_ATTN_STREAMK", 1) != 0 && env_int("PELICA_ATTN_SPLIT_BLOCKS", 0) <= 0;
+                    tn.streamk && tn.split_blocks == 0;
     const bool big = !sk && pelica::decode_can_use_8_waves(d->hd, rt) && blocks >= 2048 && d->n_kv % 4 == 0;
     const int wg_heads = big ? 4 : 1;
     // 64-key blocks per wave: enough waves for every SIMD, each streaming
     // several blocks, so the split count (and the combine's work) stays small
-    const int target_waves = std::max(64, env_int("PELICA_ATTN_DECODE_WAVES", big ? 2048 : 1024));
-    int spw = env_int("PELICA_ATTN_SPLIT_BLOCKS", 0);
+    const int target_waves = std::max(64, tn.decode_waves ? tn.decode_waves : (big ? 2048 : 1024));
+    int spw = tn.split_blocks;
     if (spw <= 0) spw = (int)std::max<long long>(1, (blocks + target_waves - 1) / target_waves);
     auto splits = [&](int nw_, long long* keys, int* ns) {
         long long split_keys = 64LL * (nw_ / wg_heads) * spw;
@@ -156,7 +186,7 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
     // <= 2 blocks), one split per kv head — the workgroup merges its waves
     // and writes the output itself, no combine launch.
     if (d->window > 0 && !big && (ceil_div(span, 64) + 1) <= 2 * (nw / wg_heads) &&
-        env_int("PELICA_ATTN_SPLIT_BLOCKS", 0) <= 0) {
+        tn.split_blocks == 0) {
         split_keys = ((long long)d->kv_len + 63) / 64 * 64;
         n_slot = 1;
     }
@@ -174,7 +204,7 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
         // (a piece's start-up is charged as sk_restart blocks: ~15 us of
         // pipeline refill against ~1.4 us per block of a workgroup's
         // stream; 8 measured best, 6-14 within 1.5 %)
-        const int restart = std::max(0, env_int("PELICA_ATTN_SK_RESTART", 8));
+        const int restart = tn.sk_restart >= 0 ? tn.sk_restart : 8;
         const int maxblk = ceil_div(d->kv_len, 64);
         const long long bmax = (long long)d->n_seq * d->n_kv * n_rg * (maxblk + restart);
         int minb = (int)std::min<long long>(64, std::max<long long>(4, bmax / (2LL * pl->sk_grid)));
@@ -209,7 +239,7 @@ int plan_mla(const PelicaAttnDesc* d, DecodePlan* pl) {
     const int rt = R <= 16 ? 1 : R <= 32 ? 2 : 4;
     const int n_rg = ceil_div(R, 16 * rt);
     const long long blocks = (long long)ceil_div(d->kv_len, 32) * n_rg * d->n_seq;
-    const int target = std::max(1, env_int("PELICA_ATTN_MLA_WORKGROUPS", 256));
+    const int target = tuning().mla_workgroups ? tuning().mla_workgroups : 256;
     long long split_keys = 32LL * std::max<long long>(1, (blocks + target - 1) / target);
     int n_slot = ceil_div(d->kv_len, split_keys);
     while (n_slot > pelica::kMaxSlots) {
@@ -230,37 +260,17 @@ int plan_mla(const PelicaAttnDesc* d, DecodePlan* pl) {
     return PELICA_ATTN_OK;
 }
 
-// merge of externally produced partials, natural-log max (merge_dec format)
-__global__ __launch_bounds__(64) void partials_merge_kernel(int n_head, int hd, int n_parts, const float* parts,
-                                                            const float* sinks, float* out) {
-    const int h = blockIdx.x, lane = threadIdx.x;
-    const size_t stride = (size_t)n_head * (hd + 2);
-    const float* ph = parts + (size_t)h * (hd + 2);
-    const float sk = sinks ? sinks[h] : -INFINITY;
-    float M = sk;
-    for (int c = lane; c < n_parts; c += 64) M = fmaxf(M, ph[c * stride]);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-    const float ms = (M == -INFINITY) ? 0.f : M;
-    float L = 0.f;
-    for (int c = lane; c < n_parts; c += 64) L += ph[c * stride + 1] * pelica::fast_exp2((ph[c * stride] - ms) * pelica::kLog2e);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off, 64);
-    if (sinks) L += pelica::fast_exp2((sk - ms) * pelica::kLog2e);
-    const float inv = 1.f / L;
-    for (int d = lane; d < hd; d += 64) {
-        float acc = 0.f;
-        for (int c = 0; c < n_parts; ++c)
-            acc += ph[c * stride + 2 + d] * pelica::fast_exp2((ph[c * stride] - ms) * pelica::kLog2e);
-        out[(size_t)h * hd + d] = acc * inv;
-    }
-}
-
 }  // namespace
 
 extern "C" {
 
 int pelica_attn_version(void) { return PELICA_ATTN_VERSION; }
+
+int pelica_attn_reload_tuning(void) {
+    g_err[0] = 0;
+    tuning_slot() = read_tuning();
+    return PELICA_ATTN_OK;
+}
 
 const char* pelica_attn_last_error(void) { return g_err; }
 
@@ -548,18 +558,25 @@ int pelica_attn_prefill_round(const PelicaAttnDesc* desc, const uint16_t* q, con
     return PELICA_ATTN_OK;
 }
 
-int pelica_attn_partials_merge(int32_t n_head, int32_t hd, int32_t n_parts, const float* parts, const float* sinks,
-                               float* out, void* stream) {
+int pelica_attn_partials_merge_batch(int32_t n_tokens, int32_t n_head, int32_t hd, int32_t n_parts,
+                                     const float* parts, const float* sinks, float* out, void* stream) {
     g_err[0] = 0;
-    if (n_head <= 0 || hd <= 0 || n_parts <= 0)
-        return fail(PELICA_ATTN_EINVAL, "n_head %d, hd %d and n_parts %d must be positive", n_head, hd, n_parts);
+    if (n_tokens <= 0 || n_tokens > 65535 || n_head <= 0 || n_parts <= 0)
+        return fail(PELICA_ATTN_EINVAL, "n_tokens %d (<= 65535), n_head %d and n_parts %d must be positive", n_tokens,
+                    n_head, n_parts);
+    if (hd <= 0 || hd % 2 || hd > 1024) return fail(PELICA_ATTN_EINVAL, "hd %d must be even, in [2, 1024]", hd);
     if (!parts || !out) return fail(PELICA_ATTN_EINVAL, "parts and out must be non-NULL");
-    pelica::ProfScope ps(pelica::kProfMerge, static_cast<hipStream_t>(stream));
-    hipLaunchKernelGGL(partials_merge_kernel, dim3(n_head), dim3(64), 0, static_cast<hipStream_t>(stream), n_head, hd,
-                       n_parts, parts, sinks, out);
-    hipError_t e = hipGetLastError();
+    if (reinterpret_cast<uintptr_t>(parts) % 8 || reinterpret_cast<uintptr_t>(out) % 8)
+        return fail(PELICA_ATTN_EINVAL, "parts and out must be 8-byte aligned");
+    hipError_t e = pelica::launch_partials_merge(n_tokens, n_head, hd, n_parts, parts, sinks, out,
+                                                 static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(PELICA_ATTN_EHIP, "merge launch: %s", hipGetErrorString(e));
     return PELICA_ATTN_OK;
+}
+
+int pelica_attn_partials_merge(int32_t n_head, int32_t hd, int32_t n_parts, const float* parts, const float* sinks,
+                               float* out, void* stream) {
+    return pelica_attn_partials_merge_batch(1, n_head, hd, n_parts, parts, sinks, out, stream);
 }
 
 }  // extern "C"

@@ -83,6 +83,12 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t 
                                              0, 0);
 }
 
+// Keys of sequence s: seq_len[s] clipped to kv_len (the bound every launch
+// and workspace is sized from), or kv_len without a per-sequence table.
+__device__ __forceinline__ int seq_keys(const int32_t* seq_len, int s, int kv_len) {
+    return seq_len ? min(seq_len[s], kv_len) : kv_len;
+}
+
 // Split x into f16 hi + lo with x ~= hi + lo to ~2^-22 relative.
 __device__ __forceinline__ void split_f16(float x, _Float16& hi, _Float16& lo) {
     hi = (_Float16)x;

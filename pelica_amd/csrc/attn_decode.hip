@@ -211,7 +211,7 @@ __device__ __forceinline__ long long uniform64(long long x) {
 
 // blocks of sequence s in the stream-K list (0 for a skipped sequence)
 __device__ __forceinline__ int sk_blocks(const DecodeParams& p, int s) {
-    const int len = p.seq_len[s];
+    const int len = seq_keys(p.seq_len, s, p.kv_len);
     return (len < p.T || len <= 0) ? 0 : (len + 63) / 64;
 }
 // list positions of one segment of sequence s (start-up + blocks, or 0)
@@ -626,7 +626,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
 
     if (!SK) {
         const int slot = blockIdx.x, by = blockIdx.y, s = blockIdx.z;
-        const int len = p.seq_len ? p.seq_len[s] : p.kv_len;
+        const int len = seq_keys(p.seq_len, s, p.kv_len);
         if (len < p.T || len <= 0) return;
         const int split0 = key_range(len, p.T, 0, p.window).lo / p.split_keys;
         const int n_active = min(p.n_slot, (len - 1) / p.split_keys - split0 + 1);
@@ -672,7 +672,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
             ++s;
             continue;
         }
-        const int len = __builtin_amdgcn_readfirstlane(p.seq_len[s]);
+        const int len = __builtin_amdgcn_readfirstlane(seq_keys(p.seq_len, s, p.kv_len));
         const int by = (int)((cur - pre) / span);
         const long long seg = pre + (long long)by * span + p.sk_restart;  // the segment's first block
         if (cur < seg) {  // (in the start-up positions)
@@ -716,7 +716,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
     const int r = ROW_WAVES ? blockIdx.x * 4 + wave : blockIdx.x / NQ, dq = ROW_WAVES ? 0 : blockIdx.x % NQ;
     const int kvh = blockIdx.y, s = blockIdx.z;
     if (ROW_WAVES && r >= p.R) return;
-    const int len = p.seq_len ? p.seq_len[s] : p.kv_len;
+    const int len = seq_keys(p.seq_len, s, p.kv_len);
     if (len < p.T || len <= 0) return;
     const int t = r / p.hpk, h = kvh * p.hpk + r % p.hpk;
     int c0, c1;  // the splits that hold keys of this row

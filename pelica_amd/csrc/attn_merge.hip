@@ -1,0 +1,122 @@
+// Merge of externally produced partial slots (the reference's merge_dec
+// format: {M natural-log max, L, O[hd]} per slot, token and head) into the
+// attention output, with optional sinks.
+//
+// Grid (n_head, n_tokens): one 512-thread workgroup per (token, head), as
+// ATTN_M's grid (n_head, TMAX) (src/oss_batch.rs:395-425).  As merge_dec_fast
+// does (src/moe_kernels.rs:750-808), each slot's weight e^(M_c - M) is
+// computed once, by one thread, into LDS (tiles of kTile slots); then thread
+// (phase, dim pair) sums its phase's slots c = phase (mod phases) with those
+// weights, 16 loads in flight at a time, and the phases are added in a fixed
+// order through LDS — the result does not depend on timing.
+#include "attn_common.hpp"
+#include "attn_merge.hpp"
+#include "attn_prof.hpp"
+
+namespace pelica {
+
+namespace {
+
+constexpr int kThreads = 512;
+constexpr int kTile = 2048;   // slot weights staged in LDS per pass
+constexpr int kBatch = 16;    // slot loads in flight per thread
+
+__device__ __forceinline__ float block_reduce(float x, float* red, bool is_max) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float y = __shfl_xor(x, off, 64);
+        x = is_max ? fmaxf(x, y) : x + y;
+    }
+    if (lane == 0) red[wave] = x;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int w = 1; w < kThreads / 64; ++w) r = is_max ? fmaxf(r, red[w]) : r + red[w];
+    __syncthreads();
+    return r;
+}
+
+__global__ __launch_bounds__(kThreads) void partials_merge_kernel(int n_tok, int n_head, int hd, int n_parts,
+                                                                  const float* __restrict__ parts,
+                                                                  const float* __restrict__ sinks,
+                                                                  float* __restrict__ out) {
+    __shared__ float w_s[kTile];
+    __shared__ float red[kThreads / 64];
+    __shared__ float2 acc_s[kThreads];
+    const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    const size_t stride = (size_t)n_tok * n_head * (hd + 2);  // floats between slots
+    const float* ph = parts + ((size_t)t * n_head + h) * (hd + 2);
+    const int dp_n = hd / 2;                   // dim pairs (hd <= 1024: <= 512)
+    const int n_ph = kThreads / dp_n;          // slot phases
+    const int ph_i = tid / dp_n, dp = tid % dp_n;
+    const bool worker = ph_i < n_ph;
+
+    // the largest max (natural log), the sink's included
+    const float sk = sinks ? sinks[h] : -INFINITY;
+    float M = sk;
+    for (int c = tid; c < n_parts; c += kThreads) M = fmaxf(M, ph[c * stride]);
+    M = block_reduce(M, red, true);
+    const float ms = (M == -INFINITY) ? 0.f : M;
+
+    float L = 0.f;
+    float2 o = make_float2(0.f, 0.f);
+    for (int t0 = 0; t0 < n_parts; t0 += kTile) {
+        const int n = min(kTile, n_parts - t0);
+        // each slot's weight, once
+        for (int x = tid; x < n; x += kThreads) {
+            const float2 ml = *reinterpret_cast<const float2*>(ph + (size_t)(t0 + x) * stride);
+            const float w = fast_exp2((ml.x - ms) * kLog2e);
+            w_s[x] = w;
+            L += ml.y * w;
+        }
+        __syncthreads();
+        if (worker) {
+            const float* po = ph + 2 + 2 * dp;
+            for (int x0 = ph_i; x0 < n; x0 += n_ph * kBatch) {
+                float2 v[kBatch];
+#pragma unroll
+                for (int j = 0; j < kBatch; ++j) {
+                    const int x = x0 + n_ph * j;
+                    v[j] = x < n ? *reinterpret_cast<const float2*>(po + (size_t)(t0 + x) * stride) : make_float2(0.f, 0.f);
+                }
+#pragma unroll
+                for (int j = 0; j < kBatch; ++j) {
+                    const int x = x0 + n_ph * j;
+                    const float w = x < n ? w_s[x] : 0.f;
+                    o.x += v[j].x * w;
+                    o.y += v[j].y * w;
+                }
+            }
+        }
+        __syncthreads();
+    }
+    L = block_reduce(L, red, false);
+    if (sinks) L += fast_exp2((sk - ms) * kLog2e);
+    // phases in order
+    acc_s[tid] = o;
+    __syncthreads();
+    if (tid < dp_n) {
+        float2 r = acc_s[tid];
+        for (int q = 1; q < n_ph; ++q) {
+            const float2 y = acc_s[q * dp_n + tid];
+            r.x += y.x;
+            r.y += y.y;
+        }
+        const float inv = 1.f / L;
+        *reinterpret_cast<float2*>(out + ((size_t)t * n_head + h) * hd + 2 * tid) = make_float2(r.x * inv, r.y * inv);
+    }
+}
+
+}  // namespace
+
+hipError_t launch_partials_merge(int n_tok, int n_head, int hd, int n_parts, const float* parts, const float* sinks,
+                                 float* out, hipStream_t st) {
+    if (hd <= 0 || hd % 2 || hd > 2 * kThreads) return hipErrorInvalidValue;
+    ProfScope ps(kProfMerge, st);
+    hipLaunchKernelGGL(partials_merge_kernel, dim3(n_head, n_tok), dim3(kThreads), 0, st, n_tok, n_head, hd, n_parts,
+                       parts, sinks, out);
+    return hipGetLastError();
+}
+
+}  // namespace pelica

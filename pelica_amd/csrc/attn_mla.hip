@@ -59,7 +59,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
     const int rg = blockIdx.y, s = blockIdx.z, slot = blockIdx.x;
-    const int len = p.seq_len ? p.seq_len[s] : p.kv_len;
+    const int len = seq_keys(p.seq_len, s, p.kv_len);
     if (len < p.T || len <= 0) return;
     const int n_active = min(p.n_slot, (len - 1) / p.split_keys + 1);
     if (slot >= n_active) return;

@@ -100,7 +100,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
     const int kvh = rest % p.n_kv, s = rest / p.n_kv;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h2 = lane >> 5, c32 = lane & 31;
-    const int len = p.seq_len ? p.seq_len[s] : p.kv_len;
+    const int len = seq_keys(p.seq_len, s, p.kv_len);
     if (len < p.T || len <= 0) return;
     const int64_t row0 = p.seq_off ? p.seq_off[s] : (int64_t)s * (p.ring_cap ? p.ring_cap : p.kv_len);
     const int t0 = tb * TB;

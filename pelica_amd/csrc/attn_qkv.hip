@@ -43,7 +43,7 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(QkvParams p) {
     const int slot = (blockIdx.x * 4 + wave) * HPW + sub;
     const int t = blockIdx.y, s = blockIdx.z;
     const int n_slot = p.n_head + 2 * p.n_kv;
-    const int len = p.seq_len ? p.seq_len[s] : p.kv_len;
+    const int len = seq_keys(p.seq_len, s, p.kv_len);
     if (len < p.T || len > p.kv_len) return;  // (attention skips such sequences too)
     // lanes of slots past the end keep to the wave's lane exchanges with
     // harmless values and store nothing

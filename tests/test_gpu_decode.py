@@ -49,9 +49,11 @@ def test_draft_tokens(T, hd, n_head, n_kv):
 
 @pytest.mark.parametrize("window", [1, 5, 128, 2000])
 @pytest.mark.parametrize("T", [1, 4])
-def test_windows(window, T):
-    cfg = wl.AttnConfig("win", "decode", 64, 8, 64, 1500, q_tokens=T, window=window, sinks=True, seed=window)
-    check(wl.make_inputs(cfg, "cuda"), f"window {window} T{T}")
+@pytest.mark.parametrize("hd,n_head,n_kv", [(64, 64, 8), (128, 32, 4), (128, 16, 16)])
+def test_windows(window, T, hd, n_head, n_kv):
+    cfg = wl.AttnConfig("win", "decode", n_head, n_kv, hd, 1500, q_tokens=T, window=window, sinks=True,
+                        seed=window + hd)
+    check(wl.make_inputs(cfg, "cuda"), f"window {window} T{T} hd{hd} h{n_head}/{n_kv}")
 
 
 def test_ragged_batch_with_minimum_lengths():
@@ -90,10 +92,15 @@ def test_ragged_batch_with_window(window, T):
 def test_stream_k_matches_grid_splits(monkeypatch):
     inp = wl.make_inputs(wl.C5.scaled(n_seq=12), "cuda")
     outs = []
-    for sk in ("0", "1"):
-        monkeypatch.setenv("PELICA_ATTN_STREAMK", sk)
-        check(inp, f"C5 x12, stream-K {sk}")
-        outs.append(as_f64(gpu_run(inp)))
+    try:
+        for sk in ("0", "1"):
+            monkeypatch.setenv("PELICA_ATTN_STREAMK", sk)
+            attn.reload_tuning()
+            check(inp, f"C5 x12, stream-K {sk}")
+            outs.append(as_f64(gpu_run(inp)))
+    finally:
+        monkeypatch.delenv("PELICA_ATTN_STREAMK")
+        attn.reload_tuning()
     assert np.abs(outs[0] - outs[1]).max() < 1e-5
 
 
@@ -102,19 +109,43 @@ def test_batch_without_offsets():
     check(wl.make_inputs(cfg, "cuda"), "n_seq 3, default offsets")
 
 
-def test_ring_buffer_window_layer():
+@pytest.mark.parametrize("hd,n_head,n_kv,T", [(64, 64, 8, 3), (128, 32, 4, 1), (128, 32, 4, 4), (128, 16, 16, 2)])
+def test_ring_buffer_window_layer(hd, n_head, n_kv, T):
     # the window layer's ring (src/oss.rs:570-572): position j in row j % cap
-    cap, L, T, W = 160, 5000, 3, 128
-    cfg = wl.AttnConfig("ring", "decode", 64, 8, 64, L, q_tokens=T, window=W, sinks=True, seed=33)
+    cap, L, W = 160, 5000, 128
+    cfg = wl.AttnConfig("ring", "decode", n_head, n_kv, hd, L, q_tokens=T, window=W, sinks=True, seed=33 + hd + T)
     inp = wl.make_inputs(cfg, "cuda")
-    kr = torch.zeros(cap, 8, 64, dtype=torch.float16, device="cuda")
+    kr = torch.zeros(cap, n_kv, hd, dtype=torch.float16, device="cuda")
     vr = torch.zeros_like(kr)
     idx = torch.arange(L - cap, L, device="cuda")
     kr[idx % cap] = inp.k[idx]
     vr[idx % cap] = inp.v[idx]
+    print(f"[case] ring hd{hd} h{n_head}/{n_kv} T{T}", flush=True)
     got = gpu_run(inp, ring_cap=cap, k=kr, v=vr)
     ref = oracle_run(inp)  # linear cache, same keys
-    assert_close(as_f64(got), as_f64(ref), what="ring")
+    assert_close(as_f64(got), as_f64(ref), what=f"ring hd{hd} T{T}")
+
+
+@pytest.mark.parametrize("hd,n_head,n_kv,T,n_seq,window", [(64, 64, 8, 1, 5, 0), (128, 32, 4, 4, 6, 0),
+                                                            (64, 64, 8, 2, 4, 500), (128, 16, 16, 1, 3, 2000)])
+def test_device_lengths_above_kv_len_are_clipped(hd, n_head, n_kv, T, n_seq, window):
+    # seq_kv_len entries above the kv_len bound (e.g. a graph replayed after
+    # the lengths grew) are clipped to kv_len: the result is that of kv_len
+    # keys, no workspace slot or cache row past the bound is touched
+    # every sequence owns L cache rows, so the clipped lengths stay inside them
+    L = 3000
+    cfg = wl.AttnConfig("clip", "decode", n_head, n_kv, hd, L, q_tokens=T, n_seq=n_seq, window=window, sinks=True,
+                        seed=91 + hd)
+    inp = wl.make_inputs(cfg, "cuda")
+    lens = torch.tensor([L + 5000] + [700 + 300 * i for i in range(n_seq - 2)] + [L + 64], dtype=torch.int32,
+                        device="cuda")
+    print(f"[case] clipped lengths hd{hd} T{T} window {window}", flush=True)
+    got = attn.decode(inp.q, inp.k, inp.v, n_kv=n_kv, kv_len=L, sinks=inp.sinks, window=window, seq_kv_len=lens,
+                      seq_kv_offset=inp.seq_off)
+    torch.cuda.synchronize()
+    inp.seq_len.copy_(lens.clamp(max=L))
+    ref = oracle_run(inp)
+    assert_close(as_f64(got), as_f64(ref), what="clipped lengths")
 
 
 def test_padded_row_stride():
@@ -134,9 +165,14 @@ def test_split_count_invariance(monkeypatch):
     # the result does not depend on how the keys are split (fixed-order merge)
     inp = wl.make_inputs(wl.C3_FULL.scaled(kv_len=9000), "cuda")
     outs = []
-    for sb in ("1", "3", "16", "200"):
-        monkeypatch.setenv("PELICA_ATTN_SPLIT_BLOCKS", sb)
-        outs.append(as_f64(gpu_run(inp)))
+    try:
+        for sb in ("1", "3", "16", "200"):
+            monkeypatch.setenv("PELICA_ATTN_SPLIT_BLOCKS", sb)
+            attn.reload_tuning()
+            outs.append(as_f64(gpu_run(inp)))
+    finally:
+        monkeypatch.delenv("PELICA_ATTN_SPLIT_BLOCKS")
+        attn.reload_tuning()
     for o in outs[1:]:
         assert np.abs(o - outs[0]).max() < 2e-6
 

@@ -138,3 +138,66 @@ def test_decode_reads_host_visible_cache():
         torch.cuda.synchronize()
         for h in host:
             hip.hipHostFree(h)
+
+
+@pytest.mark.parametrize("n_head,n_kv,hd,T,L,nv", [(64, 8, 64, 4, 6000, 4000), (32, 4, 128, 4, 5000, 3000),
+                                                    (32, 4, 128, 8, 2100, 2048)])
+def test_draft_pass_joins_cpu_tier_batched(n_head, n_kv, hd, T, L, nv):
+    # a draft-verify pass whose cache spills past the GPU: keys [0, nv) on
+    # the GPU (every draft sees all of them), [nv, L) on the CPU tier (draft
+    # t sees up to its own position L - T + t); one batched merge of all the
+    # drafts' slots with the sinks == attention over the whole cache
+    print(f"[case] drafts vram+cpu h{n_head}/{n_kv} hd{hd} T{T} L{L} nv{nv}", flush=True)
+    cfg = wl.AttnConfig("tierT", "decode", n_head, n_kv, hd, L, q_tokens=T, sinks=True, seed=nv + T)
+    inp = wl.make_inputs(cfg, "cuda")
+    # the GPU's slot: the T drafts as T one-token rows over the same nv rows
+    lens = torch.full((T,), nv, dtype=torch.int32, device="cuda")
+    offs = torch.zeros(T, dtype=torch.int64, device="cuda")
+    qg = inp.q.reshape(T, 1, n_head, hd).contiguous()
+    gpu = attn.decode_partials(qg, inp.k[:nv].contiguous(), inp.v[:nv].contiguous(), n_kv=n_kv, kv_len=nv,
+                               seq_kv_len=lens, seq_kv_offset=offs)
+    torch.cuda.synchronize()
+    q = inp.q.cpu().numpy()
+    cpu = [orc.partials(q, to_np_f16(inp.k), to_np_f16(inp.v), n_kv=n_kv, kv_len=L, t=t, k_begin=nv, k_end=L)
+           for t in range(T)]
+    n_cpu = max(len(c) for c in cpu)
+    slots = np.zeros((2 + n_cpu, T, n_head, hd + 2), np.float32)
+    slots[:, :, :, 0] = -3e38
+    slots[0] = gpu.cpu().numpy()[:, 0]
+    for t, c in enumerate(cpu):     # slot 1 stays empty; each draft's chunks after it
+        slots[2:2 + len(c), t] = c
+    out = attn.partials_merge_batch(torch.from_numpy(slots).cuda(), sinks=inp.sinks)
+    torch.cuda.synchronize()
+    assert_close(as_f64(out), as_f64(oracle_run(inp))[0], what="drafts vram + cpu tier")
+
+
+@pytest.mark.parametrize("n_parts", [1, 3, 700, 2500])
+def test_partials_merge_batch_matches_per_token(n_parts):
+    # the batched merge of (token, head) rows equals the one-token merge of
+    # each row, and the fp64 merge formula (a textbook log-sum-exp), on
+    # random slots with empties among them
+    print(f"[case] merge batch n_parts {n_parts}", flush=True)
+    rng = np.random.default_rng(n_parts)
+    T, H, hd = 3, 16, 128
+    parts = np.empty((n_parts, T, H, hd + 2), np.float32)
+    parts[..., 0] = rng.normal(0, 4, (n_parts, T, H))
+    parts[..., 1] = rng.uniform(0.5, 40, (n_parts, T, H))
+    parts[..., 2:] = rng.normal(0, 3, (n_parts, T, H, hd))
+    if n_parts > 2:
+        parts[1::3, :, :, 0] = -3e38
+    sinks = rng.normal(0, 1, H).astype(np.float32)
+    dp = torch.from_numpy(parts).cuda()
+    ds = torch.from_numpy(sinks).cuda()
+    out = attn.partials_merge_batch(dp, sinks=ds)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().astype(np.float64)
+    p = parts.astype(np.float64)
+    M = np.maximum(p[..., 0].max(axis=0), sinks[None, :])
+    w = np.exp(p[..., 0] - M[None])
+    L = (p[..., 1] * w).sum(axis=0) + np.exp(sinks[None, :] - M)
+    ref = (p[..., 2:] * w[..., None]).sum(axis=0) / L[..., None]
+    assert_close(got, ref, what="batched merge vs fp64")
+    for t in range(T):
+        one = attn.partials_merge(dp[:, t].contiguous(), n_head=H, hd=hd, sinks=ds)
+        torch.cuda.synchronize()
+        assert np.array_equal(one.cpu().numpy(), out[t].cpu().numpy()), f"token {t}"

@@ -15,14 +15,13 @@ from tests.refimpl import assert_close
 pytestmark = pytest.mark.gpu
 
 
-def test_c4_full_causal_sampled_rows():
+def test_c4_full_causal_all_rows():
+    # every one of the 4096 prompt rows x 64 heads against the oracle
     inp = wl.make_inputs(wl.C4_FULL, "cuda")
     print("[case] c4 full", flush=True)
     got = as_f64(gpu_run(inp))
-    for t0, t1 in ((0, 96), (1000, 1040), (2047, 2112), (4000, 4096)):
-        ref = as_f64(oracle_run(inp, t_begin=t0, t_end=t1))
-        assert_close(got[:, t0:t1], ref[:, t0:t1], what=f"c4 full tokens {t0}..{t1}")
-    assert np.isfinite(got).all()
+    ref = as_f64(oracle_run(inp))
+    assert_close(got, ref, what="c4 full causal, all rows")
 
 
 def test_c4_window_all_rows():
@@ -43,11 +42,13 @@ def test_small_prompts(T, hd, n_head, n_kv):
 
 
 @pytest.mark.parametrize("window", [1, 17, 64, 128, 1000])
-def test_windows(window):
-    cfg = wl.AttnConfig("pw", "prefill", 64, 8, 64, 700, q_tokens=700, window=window, sinks=True, seed=window)
+@pytest.mark.parametrize("hd,n_head,n_kv", [(64, 64, 8), (128, 32, 4)])
+def test_windows(window, hd, n_head, n_kv):
+    cfg = wl.AttnConfig("pw", "prefill", n_head, n_kv, hd, 700, q_tokens=700, window=window, sinks=True,
+                        seed=window + hd)
     inp = wl.make_inputs(cfg, "cuda")
-    print(f"[case] prefill window {window}", flush=True)
-    assert_close(as_f64(gpu_run(inp)), as_f64(oracle_run(inp)), what=f"window {window}")
+    print(f"[case] prefill window {window} hd{hd}", flush=True)
+    assert_close(as_f64(gpu_run(inp)), as_f64(oracle_run(inp)), what=f"window {window} hd{hd}")
 
 
 def test_prompt_after_cached_prefix():
@@ -65,18 +66,19 @@ def test_ragged_sequences():
     assert_close(as_f64(gpu_run(inp)), as_f64(oracle_run(inp)), what="ragged")
 
 
-def test_ring_window_prefill():
+@pytest.mark.parametrize("hd,n_head,n_kv", [(64, 64, 8), (128, 32, 4)])
+def test_ring_window_prefill(hd, n_head, n_kv):
     cap, L, T, W = 128 + 512, 3000, 512, 128
-    cfg = wl.AttnConfig("pring", "prefill", 64, 8, 64, L, q_tokens=T, window=W, sinks=True, seed=73)
+    cfg = wl.AttnConfig("pring", "prefill", n_head, n_kv, hd, L, q_tokens=T, window=W, sinks=True, seed=73 + hd)
     inp = wl.make_inputs(cfg, "cuda")
-    kr = torch.zeros(cap, 8, 64, dtype=torch.float16, device="cuda")
+    kr = torch.zeros(cap, n_kv, hd, dtype=torch.float16, device="cuda")
     vr = torch.zeros_like(kr)
     idx = torch.arange(L - cap, L, device="cuda")
     kr[idx % cap] = inp.k[idx]
     vr[idx % cap] = inp.v[idx]
-    print("[case] prefill ring", flush=True)
+    print(f"[case] prefill ring hd{hd}", flush=True)
     got = gpu_run(inp, ring_cap=cap, k=kr, v=vr)
-    assert_close(as_f64(got), as_f64(oracle_run(inp)), what="prefill ring")
+    assert_close(as_f64(got), as_f64(oracle_run(inp)), what=f"prefill ring hd{hd}")
 
 
 def test_prefill_matches_decode_rows():

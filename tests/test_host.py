@@ -122,3 +122,31 @@ def test_small_inputs_are_deterministic():
     a = wl.make_inputs(wl.C3_FULL.scaled(kv_len=256))
     b = wl.make_inputs(wl.C3_FULL.scaled(kv_len=256))
     assert (a.q == b.q).all() and (a.k == b.k).all() and (a.sinks == b.sinks).all()
+
+
+def test_partials_merge_batch_arguments():
+    lib = attn.load_library()
+    f = lib.pelica_attn_partials_merge_batch
+    assert f(0, 8, 64, 1, 16, None, 16, None) == attn.EINVAL       # no tokens
+    assert f(2, 8, 63, 1, 16, None, 16, None) == attn.EINVAL       # odd hd
+    assert f(2, 8, 2048, 1, 16, None, 16, None) == attn.EINVAL     # hd too large
+    assert f(2, 8, 64, 0, 16, None, 16, None) == attn.EINVAL       # no slots
+    assert f(2, 8, 64, 1, None, None, 16, None) == attn.EINVAL     # no parts
+    assert f(2, 8, 64, 1, 12, None, 16, None) == attn.EINVAL       # misaligned
+    assert b"aligned" in lib.pelica_attn_last_error()
+
+
+def test_planner_switches_are_read_once():
+    # the workspace size is fixed by the environment at the first plan
+    import subprocess
+    import sys
+
+    code = ("import ctypes, os\n"
+            "from pelica_amd import attn\n"
+            "d = attn.make_desc(64, 8, 64, kv_len=32768)\n"
+            "a = attn.workspace_bytes(d)\n"
+            "os.environ['PELICA_ATTN_SPLIT_BLOCKS'] = '1'\n"
+            "b = attn.workspace_bytes(d)\n"
+            "print(a == b and a > 0)\n")
+    r = subprocess.run([sys.executable, "-c", code], cwd=ROOT, capture_output=True, text=True, timeout=120)
+    assert r.stdout.strip() == "True", r.stderr
