@@ -111,6 +111,24 @@ int pelica_attn_decode(const PelicaAttnDesc* desc, const float* q, const uint16_
                        const uint16_t* v, const float* sinks, float* out,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/* Decode without a workspace argument, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  The same pass and result
+ * as pelica_attn_decode, with its split partials in a static device array
+ * of PELICA_ATTN_NOALLOC_SCRATCH_BYTES that each GPU the library runs on
+ * holds until the process ends; a pass that needs more (see
+ * pelica_attn_workspace_bytes) is rejected with PELICA_ATTN_EWORKSPACE.
+ * The call allocates nothing.  Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (other streams, other threads) race
+ * and must be ordered by the caller, e.g. on one stream.  The array's
+ * contents need no clearing between calls (each pass writes every scratch
+ * value it reads).  The first call on a device looks up its copy of the
+ * array with that device current; `stream` must belong to the current
+ * device. */
+#define PELICA_ATTN_NOALLOC_SCRATCH_BYTES (16u << 20)
+int pelica_attn_decode_noalloc(const PelicaAttnDesc* desc, const float* q, const uint16_t* k,
+                               const uint16_t* v, const float* sinks, float* out, void* stream);
+
 /* Decode partials: the same pass as pelica_attn_decode, but instead of the
  * output it writes the (max, sum, unnormalised O) of the keys this cache
  * holds, one slot per (sequence, token, head) in merge_dec's format:

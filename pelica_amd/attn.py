@@ -36,6 +36,7 @@ EXPORTS = (
     "pelica_attn_workspace_bytes",
     "pelica_attn_workspace_init",
     "pelica_attn_decode",
+    "pelica_attn_decode_noalloc",
     "pelica_attn_decode_partials",
     "pelica_attn_mla_workspace_bytes",
     "pelica_attn_mla",
@@ -152,6 +153,8 @@ def load_library() -> ctypes.CDLL:
     lib.pelica_attn_workspace_init.argtypes = [vp, sz, vp]
     lib.pelica_attn_decode.restype = ctypes.c_int
     lib.pelica_attn_decode.argtypes = [dp, vp, vp, vp, vp, vp, vp, sz, vp]
+    lib.pelica_attn_decode_noalloc.restype = ctypes.c_int
+    lib.pelica_attn_decode_noalloc.argtypes = [dp, vp, vp, vp, vp, vp, vp]
     lib.pelica_attn_decode_partials.restype = ctypes.c_int
     lib.pelica_attn_decode_partials.argtypes = [dp, vp, vp, vp, vp, vp, sz, vp]
     lib.pelica_attn_prefill.restype = ctypes.c_int
@@ -266,6 +269,33 @@ def decode(q, k, v, *, n_kv: int, kv_len: int, sinks=None, window: int = 0, ring
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     _check(lib.pelica_attn_decode(ctypes.byref(desc), _ptr(q), _ptr(k), _ptr(v), _ptr(sinks), _ptr(out),
                                   _ptr(workspace), ws_bytes, _stream_ptr(stream)))
+    return out
+
+
+#: scratch bytes of the no-allocation decode (PELICA_ATTN_NOALLOC_SCRATCH_BYTES)
+NOALLOC_SCRATCH_BYTES = 16 << 20
+
+
+def decode_noalloc(q, k, v, *, n_kv: int, kv_len: int, sinks=None, window: int = 0, ring_cap: int = 0,
+                   scale: Optional[float] = None, seq_kv_len=None, seq_kv_offset=None, kv_row_stride: int = 0,
+                   out=None, stream=None):
+    """``decode`` through pelica_attn_decode_noalloc: no workspace, the
+    library's per-device static scratch (calls on one GPU must not overlap)."""
+    import torch
+
+    assert q.dtype == torch.float32 and q.dim() == 4 and q.is_contiguous() and q.is_cuda
+    assert k.dtype == torch.float16 and v.dtype == torch.float16 and k.is_contiguous() and v.is_contiguous()
+    _validate_lens(seq_kv_len, seq_kv_offset)
+    n_seq, T, n_head, hd = q.shape
+    desc = make_desc(n_head, n_kv, hd, n_seq=n_seq, q_tokens=T, kv_len=kv_len, seq_kv_len=seq_kv_len,
+                     seq_kv_offset=seq_kv_offset, kv_row_stride=kv_row_stride, window=window,
+                     ring_cap=ring_cap, scale=scale)
+    if out is None:
+        out = torch.empty_like(q)
+    if sinks is not None:
+        assert sinks.dtype == torch.float32 and sinks.is_cuda and sinks.numel() == n_head
+    _check(load_library().pelica_attn_decode_noalloc(ctypes.byref(desc), _ptr(q), _ptr(k), _ptr(v), _ptr(sinks),
+                                                     _ptr(out), _stream_ptr(stream)))
     return out
 
 

@@ -5,6 +5,8 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <atomic>
+#include <mutex>
 
 #include "../../include/pelica_attn.h"
 #include "attn_decode.hpp"
@@ -352,9 +354,61 @@ int run_decode(const PelicaAttnDesc* desc, const float* q, const uint16_t* k, co
     return PELICA_ATTN_OK;
 }
 
+// Scratch of pelica_attn_decode_noalloc: a file-scope device array, one
+// copy per GPU the library runs on, held until the process ends.  In host
+// code `scratch` names a host-side stand-in, never the device memory: host
+// code uses only the per-device address from hipGetSymbolAddress below.
+static __device__ __align__(256) char scratch[PELICA_ATTN_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// This device's copy of `scratch`, looked up on the first call on the device
+// (with that device current) and kept.
+int scratch_of_current_device(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(PELICA_ATTN_EHIP, "hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return fail(PELICA_ATTN_EUNSUPPORTED, "device %d (at most %d)", dev, kMaxDevices);
+    void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+        if (!p) {
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || !p)
+                return fail(PELICA_ATTN_EHIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+            g_scratch_ptr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return PELICA_ATTN_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int pelica_attn_decode_noalloc(const PelicaAttnDesc* desc, const float* q, const uint16_t* k, const uint16_t* v,
+                               const float* sinks, float* out, void* stream) {
+    g_err[0] = 0;
+    DecodePlan pl;
+    int rc = plan_decode(desc, &pl);
+    if (rc) return rc;
+    if (desc->flags) return fail(PELICA_ATTN_EINVAL, "flags must be 0");
+    if (pl.ws_bytes > PELICA_ATTN_NOALLOC_SCRATCH_BYTES)
+        return fail(PELICA_ATTN_EWORKSPACE, "this pass needs %zu bytes of scratch, above the %zu of the no-allocation "
+                    "entry point (use pelica_attn_decode with a workspace)", pl.ws_bytes,
+                    (size_t)PELICA_ATTN_NOALLOC_SCRATCH_BYTES);
+    void* ws = nullptr;
+    if (pl.ws_bytes) {
+        rc = scratch_of_current_device(&ws);
+        if (rc) return rc;
+    }
+    return run_decode(desc, q, k, v, sinks, out, nullptr, ws, pl.ws_bytes ? PELICA_ATTN_NOALLOC_SCRATCH_BYTES : 0,
+                      stream);
+}
 
 int pelica_attn_decode(const PelicaAttnDesc* desc, const float* q, const uint16_t* k, const uint16_t* v,
                        const float* sinks, float* out, void* workspace, size_t workspace_bytes, void* stream) {

@@ -150,3 +150,23 @@ def test_planner_switches_are_read_once():
             "print(a == b and a > 0)\n")
     r = subprocess.run([sys.executable, "-c", code], cwd=ROOT, capture_output=True, text=True, timeout=120)
     assert r.stdout.strip() == "True", r.stderr
+
+
+def test_noalloc_decode_rejects_oversize_pass():
+    # a pass whose partials exceed the static scratch is refused before any
+    # GPU call (a 64-sequence stream-K verify batch at 64K keys: ~77 MB)
+    d = _desc(n_head=32, n_kv=4, hd=128, n_seq=64, q_tokens=4, kv_len=1 << 16)
+    d.seq_kv_len, d.seq_kv_offset = 256, 512   # device tables (not read by the planner)
+    need = attn.workspace_bytes(d)
+    assert need > attn.NOALLOC_SCRATCH_BYTES
+    lib = attn.load_library()
+    rc = lib.pelica_attn_decode_noalloc(ctypes.byref(d), 16, 16, 16, None, 16, None)
+    assert rc == attn.EWORKSPACE and b"scratch" in lib.pelica_attn_last_error()
+    d.flags = attn.FLAG_SPLIT_ONLY
+    assert lib.pelica_attn_decode_noalloc(ctypes.byref(d), 16, 16, 16, None, 16, None) == attn.EINVAL
+
+
+def test_noalloc_scratch_size_matches_header():
+    text = open(os.path.join(ROOT, "include", "pelica_attn.h")).read()
+    m = re.search(r"#define PELICA_ATTN_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", text)
+    assert m and int(m.group(1)) << int(m.group(2)) == attn.NOALLOC_SCRATCH_BYTES
