@@ -232,10 +232,10 @@ def workspace_bytes(desc: AttnDesc) -> int:
 
 
 def new_workspace(desc: AttnDesc, device="cuda"):
-    """A workspace for decode calls with this descriptor (no init needed)."""
+    """A zero-filled workspace for decode calls with this descriptor."""
     import torch
 
-    return torch.empty(max(workspace_bytes(desc), 16), dtype=torch.uint8, device=device)
+    return torch.zeros(max(workspace_bytes(desc), 16), dtype=torch.uint8, device=device)
 
 
 def decode(q, k, v, *, n_kv: int, kv_len: int, sinks=None, window: int = 0, ring_cap: int = 0,
@@ -263,7 +263,7 @@ def decode(q, k, v, *, n_kv: int, kv_len: int, sinks=None, window: int = 0, ring
     if out is None:
         out = torch.empty_like(q)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
-        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+        workspace = torch.zeros(need, dtype=torch.uint8, device=q.device)
     if sinks is not None:
         assert sinks.dtype == torch.float32 and sinks.is_cuda and sinks.numel() == n_head
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
@@ -323,7 +323,7 @@ def decode_partials(q, k, v, *, n_kv: int, kv_len: int, window: int = 0, ring_ca
     if parts is None:
         parts = torch.empty(n_seq, T, n_head, hd + 2, dtype=torch.float32, device=q.device)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
-        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+        workspace = torch.zeros(need, dtype=torch.uint8, device=q.device)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     _check(lib.pelica_attn_decode_partials(ctypes.byref(desc), _ptr(q), _ptr(k), _ptr(v), _ptr(parts),
                                            _ptr(workspace), ws_bytes, _stream_ptr(stream)))

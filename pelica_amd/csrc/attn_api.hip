@@ -42,6 +42,8 @@ struct Tuning {
     int decode_waves;   // PELICA_ATTN_DECODE_WAVES (target waves of a split grid)
     int sk_restart;     // PELICA_ATTN_SK_RESTART (positions charged per stream-K piece start)
     int mla_workgroups; // PELICA_ATTN_MLA_WORKGROUPS
+    int fuse;           // PELICA_ATTN_FUSE (in-kernel split merge; default 0)
+    int fuse_groups;    // PELICA_ATTN_FUSE_GROUPS (level-1 groups; default 8)
 };
 
 Tuning read_tuning() {
@@ -51,6 +53,8 @@ Tuning read_tuning() {
     x.decode_waves = std::max(0, env_int("PELICA_ATTN_DECODE_WAVES", 0));
     x.sk_restart = env_int("PELICA_ATTN_SK_RESTART", -1);
     x.mla_workgroups = std::max(0, env_int("PELICA_ATTN_MLA_WORKGROUPS", 0));
+    x.fuse = env_int("PELICA_ATTN_FUSE", 0);
+    x.fuse_groups = std::max(1, env_int("PELICA_ATTN_FUSE_GROUPS", 8));
     return x;
 }
 
@@ -127,10 +131,15 @@ struct DecodePlan {
     int R, rt, n_rg, split_keys, n_slot, wg_heads, nw;
     bool sk;
     int sk_grid, sk_minb, sk_restart;
-    size_t ctr_bytes, ml_bytes, ws_bytes;
+    bool fuse;
+    int n_grp;
+    size_t ctr_bytes, ml_bytes, o_bytes, l1ml_bytes, ws_bytes;
 };
 
-int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
+// allow_fuse: the in-kernel split merge may be planned (its counters need a
+// workspace zero-filled before the first call; the no-allocation entry point
+// never uses it)
+int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl, bool allow_fuse = true) {
     int rc = check_desc(d);
     if (rc) return rc;
     const Tuning& tn = tuning();
@@ -225,10 +234,20 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl) {
     pl->nw = nw;
     // workspace: (max, sum) pairs, then O rows, 256-byte aligned parts
     const size_t n_part = (size_t)d->n_seq * d->n_kv * R * n_slot;
-    // stream-K: the piece count of each segment, then the partials
-    pl->ctr_bytes = sk ? ((size_t)d->n_seq * d->n_kv * n_rg * 4 + 255) & ~(size_t)255 : 0;
-    pl->ml_bytes = (n_part * 2 * 4 + 255) & ~(size_t)255;
-    pl->ws_bytes = n_slot > 1 ? pl->ctr_bytes + pl->ml_bytes + n_part * d->hd * 4 : 0;
+    auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    // (the fused merge addresses its partials with 31-bit byte offsets)
+    pl->fuse = allow_fuse && !sk && n_slot > 1 && tn.fuse && (size_t)d->n_seq * d->n_kv * R * n_slot * d->hd * 4 < (1u << 31);
+    pl->n_grp = pl->fuse ? std::min(tn.fuse_groups, n_slot) : 0;
+    const size_t segs = (size_t)d->n_seq * (d->n_kv / wg_heads) * n_rg;
+    // stream-K: the piece count of each segment; fused merge: the arrival
+    // counters; then the partials (and the fused merge's level-1 partials)
+    pl->ctr_bytes = sk ? al((size_t)d->n_seq * d->n_kv * n_rg * 4) : pl->fuse ? al(segs * (pl->n_grp + 1) * 4) : 0;
+    pl->ml_bytes = al(n_part * 2 * 4);
+    pl->o_bytes = al(n_part * d->hd * 4);
+    const size_t n_l1 = (size_t)d->n_seq * d->n_kv * R * pl->n_grp;
+    pl->l1ml_bytes = al(n_l1 * 2 * 4);
+    pl->ws_bytes = n_slot > 1 ? pl->ctr_bytes + pl->ml_bytes + pl->o_bytes + (pl->fuse ? pl->l1ml_bytes + n_l1 * d->hd * 4 : 0)
+                              : 0;
     return PELICA_ATTN_OK;
 }
 
@@ -300,10 +319,10 @@ namespace {
 // decode into out (final, with sinks) or into merge_dec partial slots
 int run_decode(const PelicaAttnDesc* desc, const float* q, const uint16_t* k, const uint16_t* v,
                const float* sinks, float* out, float* parts, void* workspace, size_t workspace_bytes,
-               void* stream) {
+               void* stream, bool allow_fuse = true) {
     g_err[0] = 0;
     DecodePlan pl;
-    int rc = plan_decode(desc, &pl);
+    int rc = plan_decode(desc, &pl, allow_fuse);
     if (rc) return rc;
     if (!q || !k || !v || !(out || parts))
         return fail(PELICA_ATTN_EINVAL, "q, k, v and %s must be non-NULL", parts ? "parts" : "out");
@@ -349,6 +368,15 @@ int run_decode(const PelicaAttnDesc* desc, const float* q, const uint16_t* k, co
     p.sk_restart = pl.sk_restart;
     p.rg_rows = 16 * pl.rt;
     p.ws_np = pl.sk && pl.ws_bytes ? reinterpret_cast<int*>(ws) : nullptr;
+    p.fuse = pl.fuse;
+    if (pl.fuse) {
+        const size_t segs = (size_t)desc->n_seq * (desc->n_kv / pl.wg_heads) * pl.n_rg;
+        p.n_grp = pl.n_grp;
+        p.ctr1 = reinterpret_cast<unsigned*>(ws);
+        p.ctr2 = p.ctr1 + segs * pl.n_grp;
+        p.l1_ml = reinterpret_cast<float*>(ws + pl.ctr_bytes + pl.ml_bytes + pl.o_bytes);
+        p.l1_o = reinterpret_cast<float*>(ws + pl.ctr_bytes + pl.ml_bytes + pl.o_bytes + pl.l1ml_bytes);
+    }
     hipError_t e = pelica::launch_decode(p, pl.rt, pl.nw, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(PELICA_ATTN_EHIP, "decode launch: %s", hipGetErrorString(e));
     return PELICA_ATTN_OK;
@@ -394,7 +422,7 @@ int pelica_attn_decode_noalloc(const PelicaAttnDesc* desc, const float* q, const
                                const float* sinks, float* out, void* stream) {
     g_err[0] = 0;
     DecodePlan pl;
-    int rc = plan_decode(desc, &pl);
+    int rc = plan_decode(desc, &pl, false);
     if (rc) return rc;
     if (desc->flags) return fail(PELICA_ATTN_EINVAL, "flags must be 0");
     if (pl.ws_bytes > PELICA_ATTN_NOALLOC_SCRATCH_BYTES)
@@ -407,7 +435,7 @@ int pelica_attn_decode_noalloc(const PelicaAttnDesc* desc, const float* q, const
         if (rc) return rc;
     }
     return run_decode(desc, q, k, v, sinks, out, nullptr, ws, pl.ws_bytes ? PELICA_ATTN_NOALLOC_SCRATCH_BYTES : 0,
-                      stream);
+                      stream, false);
 }
 
 int pelica_attn_decode(const PelicaAttnDesc* desc, const float* q, const uint16_t* k, const uint16_t* v,

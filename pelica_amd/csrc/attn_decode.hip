@@ -238,6 +238,153 @@ __device__ SkLayout sk_layout(const DecodeParams& p, int gy) {
     return L;
 }
 
+// Device-coherent (agent-scope) accesses of the fused merge's partials: the
+// sc1 cache policy writes a store through to the device's coherence point and
+// makes a load miss any stale copy in this CU's L1 and this XCD's L2 — the
+// same accesses the compiler emits for relaxed agent-scope atomic loads and
+// stores, at 16 bytes a lane.  Ordering comes from waiting for the stores
+// (vmcnt) before the arrival counter's atomic, and from issuing the loads
+// after the atomic has returned.  (An acq_rel counter instead writes back and
+// invalidates the whole L2 per workgroup; measured ~12 us slower on the 32K
+// gpt-oss layer.)
+constexpr int kAuxDev = 16;  // sc1
+// a buffer resource over a wave-uniform base (per-lane bases would make every
+// access a waterfall loop); offsets are in bytes, below 2^31
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const void* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, kBufferFlags);
+}
+__device__ __forceinline__ void st_dev4(const __amdgpu_buffer_rsrc_t& r, size_t off, const float4v& v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, (int)off, 0, kAuxDev);
+}
+__device__ __forceinline__ void st_dev2(const __amdgpu_buffer_rsrc_t& r, size_t off, const float2& v) {
+    __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(v.x), __float_as_uint(v.y)}, r, (int)off, 0, kAuxDev);
+}
+__device__ __forceinline__ float4v ld_dev4(const __amdgpu_buffer_rsrc_t& r, size_t off) {
+    return __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kAuxDev));
+}
+__device__ __forceinline__ float2 ld_dev2(const __amdgpu_buffer_rsrc_t& r, size_t off) {
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, kAuxDev);
+    return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
+}
+
+// slots a merging thread loads before merging them
+constexpr int kFuseBatch = 16;
+
+// (m, l, o) := (m, l, o) merged with (m2, l2, o2), base-2 maxima
+__device__ __forceinline__ void merge_state(float& m, float& l, float4v& o, float m2, float l2, const float4v& o2) {
+    const float M = fmaxf(m, m2);
+    const float ms = (M == -INFINITY) ? 0.f : M;
+    const float a = fast_exp2(m - ms), b = fast_exp2(m2 - ms);
+    l = l * a + l2 * b;
+    o = o * a + o2 * b;
+    m = M;
+}
+
+// sink in max and denominator, then 1/L (or 1/L alone): the output factor
+// of a row's merged state (m base-2 max, l sum)
+__device__ __forceinline__ float out_factor(const DecodeParams& p, int h, float m, float l) {
+    if (!p.sinks) return 1.f / l;
+    const float sk = p.sinks[h] * kLog2e;
+    const float M2 = fmaxf(m, sk);
+    const float ms = (m == -INFINITY) ? 0.f : m;
+    const float wgt = fast_exp2(ms - M2);
+    return wgt / (l * wgt + fast_exp2(sk - M2));
+}
+
+// In-kernel merge of the key splits, after this workgroup's split partials
+// are stored (see DecodeParams::fuse).  Level 1: the splits of group
+// slot % n_grp; level 2: the groups in order.  Each level's last arriver is
+// found with an agent-scope acq_rel counter: its release makes this
+// workgroup's partials (ordered before it by the barrier) visible across
+// the XCDs' L2s, its acquire makes the other workgroups' partials visible
+// to this one.  The merging threads take (row, 4 dims) items of the
+// workgroup's wg_heads kv heads.
+template <int HD, int H>
+__device__ __forceinline__ void fused_merge(const DecodeParams& p, int s, int by, int len, int slot, int n_active,
+                                         int* s_last) {
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int hgroups = p.n_kv / H, rg = by / hgroups, kv0 = (by % hgroups) * H;
+    const int rows = min(p.rg_rows, p.R - rg * p.rg_rows);  // this row group's rows
+    const int rbase = rg * p.rg_rows;
+    constexpr int Q = HD / 4;
+    const int items = H * rows * Q;
+    const int grp = slot % p.n_grp;
+    const int n_g = min(p.n_grp, n_active);            // groups with a split
+    const int cnt = (n_active - grp + p.n_grp - 1) / p.n_grp;  // splits of this group
+    wait_vm<0>();  // this wave's partial stores are done
+    __syncthreads();
+    if (tid == 0) {
+        unsigned* c = p.ctr1 + ((size_t)s * hgroups * p.n_rg + by) * p.n_grp + grp;
+        const unsigned old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = old + 1 == (unsigned)cnt;
+        if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *s_last = last;
+    }
+    __syncthreads();
+    if (!*s_last) return;
+    // level 1: this group's splits in slot order
+    for (int it = tid; it < items; it += nt) {
+        const int q4 = it % Q, rr = (it / Q) % rows, hl = it / (Q * rows);
+        const int r = rbase + rr, kvh = kv0 + hl;
+        const size_t base = ((size_t)(s * p.n_kv + kvh) * p.R + r) * p.n_slot;
+        float m = -INFINITY, l = 0.f;
+        float4v o = {0.f, 0.f, 0.f, 0.f};
+        for (int c0 = grp; c0 < n_active; c0 += kFuseBatch * p.n_grp) {
+            float2 ml[kFuseBatch];
+            float4v ov[kFuseBatch];
+#pragma unroll
+            for (int j = 0; j < kFuseBatch; ++j) {  // all loads in flight, then the merge
+                const int c = c0 + j * p.n_grp;
+                ml[j] = c < n_active ? ld_dev2(dev_rsrc(p.ws_ml), 8 * (base + c)) : make_float2(-INFINITY, 0.f);
+                ov[j] = c < n_active ? ld_dev4(dev_rsrc(p.ws_o), 4 * ((base + c) * HD + 4 * q4)) : float4v{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int j = 0; j < kFuseBatch; ++j) merge_state(m, l, o, ml[j].x, ml[j].y, ov[j]);
+        }
+        const size_t g1 = ((size_t)(s * p.n_kv + kvh) * p.R + r) * p.n_grp + grp;
+        if (q4 == 0) st_dev2(dev_rsrc(p.l1_ml), 8 * g1, make_float2(m, l));
+        st_dev4(dev_rsrc(p.l1_o), 4 * (g1 * HD + 4 * q4), o);
+    }
+    wait_vm<0>();
+    __syncthreads();
+    if (tid == 0) {
+        unsigned* c = p.ctr2 + (size_t)s * hgroups * p.n_rg + by;
+        const unsigned old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = old + 1 == (unsigned)n_g;
+        if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *s_last = last;
+    }
+    __syncthreads();
+    if (!*s_last) return;
+    // level 2: the groups in order, the sink, the output
+    for (int it = tid; it < items; it += nt) {
+        const int q4 = it % Q, rr = (it / Q) % rows, hl = it / (Q * rows);
+        const int r = rbase + rr, kvh = kv0 + hl;
+        const size_t base = ((size_t)(s * p.n_kv + kvh) * p.R + r) * p.n_grp;
+        float m = -INFINITY, l = 0.f;
+        float4v o = {0.f, 0.f, 0.f, 0.f};
+        for (int g0 = 0; g0 < n_g; g0 += kFuseBatch) {
+            float2 ml[kFuseBatch];
+            float4v ov[kFuseBatch];
+#pragma unroll
+            for (int j = 0; j < kFuseBatch; ++j) {
+                const int g = g0 + j;
+                ml[j] = g < n_g ? ld_dev2(dev_rsrc(p.l1_ml), 8 * (base + g)) : make_float2(-INFINITY, 0.f);
+                ov[j] = g < n_g ? ld_dev4(dev_rsrc(p.l1_o), 4 * ((base + g) * HD + 4 * q4)) : float4v{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int j = 0; j < kFuseBatch; ++j) merge_state(m, l, o, ml[j].x, ml[j].y, ov[j]);
+        }
+        const int t = r / p.hpk, h = kvh * p.hpk + r % p.hpk;
+        if (p.parts) {
+            store_part(p.parts + ((size_t)(s * p.T + t) * p.n_head + h) * (HD + 2), 4 * q4, m, l, o);
+        } else {
+            const float f = out_factor(p, h, m, l);
+            *reinterpret_cast<float4v*>(p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + 4 * q4) = o * f;
+        }
+    }
+}
+
 template <int HD, int RT, int NW, int H, bool SK>
 constexpr int kDecodeOccK = SK ? ((HD == 64 && RT == 1) ? kDecodeOcc<HD, RT, NW> : 1) : kDecodeOcc<HD, RT, NW>;
 
@@ -260,6 +407,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     constexpr int SMEM = WSLOT * NW;
     __shared__ __attribute__((aligned(16))) char smem[SMEM];
     __shared__ unsigned arrivals[H];  // waves of each head done (merge at the end)
+    __shared__ int s_last;            // fused merge: this workgroup arrived last
 
     // wave index as a scalar: the buffer resources built from it stay in SGPRs
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4,
@@ -616,9 +764,16 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
             for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<float4v*>(op + 16 * dt) = o[dt][rt] * f;
         } else {
             const size_t idx = ((size_t)(s * p.n_kv + kvh) * p.R + r) * p.n_slot + slot;
-            if (g == 0) *reinterpret_cast<float2*>(p.ws_ml + 2 * idx) = make_float2(M, L);
+            if (p.fuse) {
+                // device-coherent stores: another XCD's workgroup merges them
+                if (g == 0) st_dev2(dev_rsrc(p.ws_ml), 8 * idx, make_float2(M, L));
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<float4v*>(p.ws_o + idx * HD + 16 * dt + 4 * g) = o[dt][rt];
+                for (int dt = 0; dt < DT; ++dt) st_dev4(dev_rsrc(p.ws_o), 4 * (idx * HD + 16 * dt + 4 * g), o[dt][rt]);
+            } else {
+                if (g == 0) *reinterpret_cast<float2*>(p.ws_ml + 2 * idx) = make_float2(M, L);
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<float4v*>(p.ws_o + idx * HD + 16 * dt + 4 * g) = o[dt][rt];
+            }
         }
     }
     DTRACE(6);
@@ -633,6 +788,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
         if (slot >= n_active) return;
         const int kbeg = (split0 + slot) * p.split_keys;
         split(s, by, len, kbeg, min(kbeg + p.split_keys, len), slot, n_active == 1);
+        if (p.fuse && n_active > 1 && !p.split_only) fused_merge<HD, H>(p, s, by, len, slot, n_active, &s_last);
         return;
     }
     // stream-K: this workgroup's range of the block list, piece by piece
@@ -860,7 +1016,7 @@ static hipError_t launch_k(const DecodeParams& p, hipStream_t st) {
     }
     }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || p.n_slot == 1 || p.split_only) return e;
+    if (e != hipSuccess || p.n_slot == 1 || p.split_only || p.fuse) return e;
     return launch_combine(p, st);
 }
 

@@ -40,6 +40,18 @@ struct DecodeParams {
     int sk_restart;      // list positions charged at each segment's start (a piece's start-up cost)
     int* ws_np;          // stream-K: pieces of each (sequence, row group x kv head) segment
     int rg_rows;         // query rows per row group (16 x row tiles)
+    // In-kernel merge of the key splits (split grid, more than one split):
+    // the last workgroup to finish in each level-1 group of splits (slots
+    // congruent mod n_grp) merges the group's partials into l1_*, and the
+    // last group to finish merges the n_grp group results into the output.
+    // The arrival counters must be zero before the call; each call leaves
+    // them at zero.
+    bool fuse;
+    int n_grp;
+    unsigned* ctr1;      // [n_seq][n_kv / wg_heads * n_rg][n_grp]
+    unsigned* ctr2;      // [n_seq][n_kv / wg_heads * n_rg]
+    float* l1_ml;        // [n_seq][n_kv][R][n_grp] x (max, sum), base-2 max
+    float* l1_o;         // [n_seq][n_kv][R][n_grp][hd]
 };
 
 hipError_t launch_decode(const DecodeParams& p, int rt, int nw, hipStream_t st);
