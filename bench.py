@@ -223,6 +223,43 @@ def bench_qkv(steps, warmup, T=4096, n_head=64, n_kv=8, hd=64):
                 frac_hbm=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, kernel_ms=kt)
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), for the CPU baseline."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def bench_merge(steps, warmup, n_slots=512, n_tok=1, n_head=32, hd=128):
+    """pelica_attn_partials_merge_batch at the MoE engine's CPU-tier layout
+    (src/moe.rs:1713-1729: one slot per 64 positions, 512 at 32K keys;
+    Qwen3 heads): bytes = the slots read once + the output written."""
+    import torch
+
+    from pelica_amd import attn
+
+    g = torch.Generator(device="cuda").manual_seed(14)
+    parts = torch.randn(n_slots, n_tok, n_head, hd + 2, generator=g, device="cuda")
+    parts[..., 1] = parts[..., 1].abs() + 1.0
+    sinks = torch.randn(n_head, generator=g, device="cuda")
+    copies = rotating_copies(parts, 256 << 20)
+    out = torch.empty(n_tok, n_head, hd, device="cuda")
+
+    def call(i):
+        attn.partials_merge_batch(copies[i], sinks=sinks, out=out)
+
+    ms = time_calls(call, len(copies), steps, warmup)
+    kt = kernel_times(call, len(copies), steps)
+    nbytes = parts.numel() * 4 + out.numel() * 4
+    return dict(config=f"partials_merge_{n_slots}slots_t{n_tok}_h{n_head}_hd{hd}", ms=ms, bytes=nbytes,
+                GBps=nbytes / (ms * 1e-3) / 1e9, frac_hbm=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, kernel_ms=kt)
+
+
 def cpu_baseline_decode(cfg, reps=20):
     """The C port of cpu_attn.rs on every host core, full C3 workload: one
     warm-up call, then the median of `reps`."""
@@ -244,7 +281,7 @@ def cpu_baseline_decode(cfg, reps=20):
         orc.attention(q, k, v, n_kv=cfg.n_kv, kv_len=cfg.kv_len, sinks=sinks, window=cfg.window, threads=threads)
         times.append(time.perf_counter() - t)
     sec = float(np.median(times))
-    return dict(value=wl.kv_bytes(cfg) / sec / 1e9, unit="GB/s", cores=threads, kind="port",
+    return dict(value=wl.kv_bytes(cfg) / sec / 1e9, unit="GB/s", cores=threads, kind="port", model=cpu_model(),
                 sample=f"full {cfg.name} call (64 query heads x 32768 keys), median of {reps}",
                 ms=sec * 1e3)
 
@@ -277,7 +314,7 @@ def cpu_baseline_prefill(cfg, rows=32, reps=20):
     sec = float(np.median(times))
     pairs = sum(min(p + 1, cfg.window) if cfg.window else p + 1 for p in range(T - rows, T))
     flops = 4 * cfg.hd * cfg.n_head * pairs
-    return dict(value=flops / sec / 1e12, unit="TFLOP/s", cores=threads, kind="port",
+    return dict(value=flops / sec / 1e12, unit="TFLOP/s", cores=threads, kind="port", model=cpu_model(),
                 sample=f"last {rows} of {T} prompt tokens of {cfg.name}, median of {reps}", ms=sec * 1e3)
 
 
@@ -340,6 +377,10 @@ def main():
         results["mla_decode_h32_32k"] = bench_mla(args.steps, args.warmup)
     if not only or "qkv_rope_cache_gptoss_4096" in only:
         results["qkv_rope_cache_gptoss_4096"] = bench_qkv(args.steps, args.warmup)
+    for nt in (1, 4):
+        r = bench_merge(args.steps, args.warmup, n_tok=nt) if (not only or f"partials_merge_t{nt}" in only) else None
+        if r:
+            results[r["config"]] = r
 
     head = results.get(wl.C3_FULL.name)
     pre = results.get(wl.C4_FULL.name)

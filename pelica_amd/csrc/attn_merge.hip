@@ -7,8 +7,10 @@
 // does (src/moe_kernels.rs:750-808), each slot's weight e^(M_c - M) is
 // computed once, by one thread, into LDS (tiles of kTile slots); then thread
 // (phase, dim pair) sums its phase's slots c = phase (mod phases) with those
-// weights, 16 loads in flight at a time, and the phases are added in a fixed
-// order through LDS — the result does not depend on timing.
+// weights, kBatch loads in flight at a time, and the phases are added in a
+// fixed order through LDS — the result does not depend on timing.  The
+// slots' (max, sum) pairs and the first O loads are requested together with
+// the max pass, so the merge costs about one memory round trip per batch.
 #include "attn_common.hpp"
 #include "attn_merge.hpp"
 #include "attn_prof.hpp"
@@ -18,8 +20,8 @@ namespace pelica {
 namespace {
 
 constexpr int kThreads = 512;
-constexpr int kTile = 2048;   // slot weights staged in LDS per pass
-constexpr int kBatch = 16;    // slot loads in flight per thread
+constexpr int kTile = 2048;   // slot (max, sum) pairs staged in LDS per pass
+constexpr int kBatch = 32;    // O loads in flight per thread
 
 __device__ __forceinline__ float block_reduce(float x, float* red, bool is_max) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -41,7 +43,7 @@ __global__ __launch_bounds__(kThreads) void partials_merge_kernel(int n_tok, int
                                                                   const float* __restrict__ parts,
                                                                   const float* __restrict__ sinks,
                                                                   float* __restrict__ out) {
-    __shared__ float w_s[kTile];
+    __shared__ float2 ml_s[kTile];   // this tile's (max, sum) pairs, then (weight, -)
     __shared__ float red[kThreads / 64];
     __shared__ float2 acc_s[kThreads];
     const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
@@ -51,42 +53,54 @@ __global__ __launch_bounds__(kThreads) void partials_merge_kernel(int n_tok, int
     const int n_ph = kThreads / dp_n;          // slot phases
     const int ph_i = tid / dp_n, dp = tid % dp_n;
     const bool worker = ph_i < n_ph;
-
-    // the largest max (natural log), the sink's included
+    const float* po = ph + 2 + 2 * dp;
     const float sk = sinks ? sinks[h] : -INFINITY;
+
+    // the largest max (natural log) over every slot and the sink
     float M = sk;
     for (int c = tid; c < n_parts; c += kThreads) M = fmaxf(M, ph[c * stride]);
-    M = block_reduce(M, red, true);
-    const float ms = (M == -INFINITY) ? 0.f : M;
 
     float L = 0.f;
     float2 o = make_float2(0.f, 0.f);
+    float2 v[kBatch];
+    auto load_batch = [&](int t0, int n, int x0) {
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const int x = x0 + n_ph * j;
+            v[j] = worker && x < n ? *reinterpret_cast<const float2*>(po + (size_t)(t0 + x) * stride)
+                                   : make_float2(0.f, 0.f);
+        }
+    };
+    // the first tile's (max, sum) pairs into LDS and its first O batch into
+    // registers, both in flight while the max is reduced
+    int n = min(kTile, n_parts);
+    for (int x = tid; x < n; x += kThreads) ml_s[x] = *reinterpret_cast<const float2*>(ph + (size_t)x * stride);
+    load_batch(0, n, ph_i);
+    M = block_reduce(M, red, true);  // (its barriers also publish ml_s)
+    const float ms = (M == -INFINITY) ? 0.f : M;
     for (int t0 = 0; t0 < n_parts; t0 += kTile) {
-        const int n = min(kTile, n_parts - t0);
+        n = min(kTile, n_parts - t0);
+        if (t0 > 0) {
+            for (int x = tid; x < n; x += kThreads) ml_s[x] = *reinterpret_cast<const float2*>(ph + (size_t)(t0 + x) * stride);
+            load_batch(t0, n, ph_i);
+            __syncthreads();
+        }
         // each slot's weight, once
         for (int x = tid; x < n; x += kThreads) {
-            const float2 ml = *reinterpret_cast<const float2*>(ph + (size_t)(t0 + x) * stride);
+            const float2 ml = ml_s[x];
             const float w = fast_exp2((ml.x - ms) * kLog2e);
-            w_s[x] = w;
+            ml_s[x].x = w;
             L += ml.y * w;
         }
         __syncthreads();
-        if (worker) {
-            const float* po = ph + 2 + 2 * dp;
-            for (int x0 = ph_i; x0 < n; x0 += n_ph * kBatch) {
-                float2 v[kBatch];
+        for (int x0 = ph_i; x0 < n; x0 += n_ph * kBatch) {
+            if (x0 != ph_i) load_batch(t0, n, x0);
 #pragma unroll
-                for (int j = 0; j < kBatch; ++j) {
-                    const int x = x0 + n_ph * j;
-                    v[j] = x < n ? *reinterpret_cast<const float2*>(po + (size_t)(t0 + x) * stride) : make_float2(0.f, 0.f);
-                }
-#pragma unroll
-                for (int j = 0; j < kBatch; ++j) {
-                    const int x = x0 + n_ph * j;
-                    const float w = x < n ? w_s[x] : 0.f;
-                    o.x += v[j].x * w;
-                    o.y += v[j].y * w;
-                }
+            for (int j = 0; j < kBatch; ++j) {
+                const int x = x0 + n_ph * j;
+                const float w = worker && x < n ? ml_s[x].x : 0.f;
+                o.x += v[j].x * w;
+                o.y += v[j].y * w;
             }
         }
         __syncthreads();
