@@ -120,10 +120,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
         (void*)(p.k + row0 * p.row_stride + (size_t)kvh * HD), (short)0, (int)nrec, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(p.v + row0 * p.row_stride + (size_t)kvh * HD), (short)0, (int)nrec, kBufferFlags);
-    const int kb0 = max(lo_first, kbeg) & ~63;
+    // 32-key chunks from the first chunk any row sees to the last: tiles of
+    // 64 keys start at kb0 (32-aligned), and the last tile may hold only one
+    // needed chunk (a 32-token block of a window-128 layer takes 5 chunks, not
+    // the 6 of 64-aligned whole tiles)
+    const int kb0 = max(lo_first, kbeg) & ~31;
     const int klast = min(pos_last, kend - 1);
-    const int n_tiles = klast >= kb0 ? (klast - kb0) / 64 + 1 : 0;  // 0: a round past these tokens
-    const int n_chunks = 2 * n_tiles;  // 32-key chunks
+    const int n_chunks = klast >= kb0 ? (klast - kb0) / 32 + 1 : 0;  // 0: a round past these tokens
+    const int n_tiles = (n_chunks + 1) / 2;
     // Tiles go from HBM straight into LDS (buffer_load ... lds): wave
     // instruction i of wave w fills LDS slots 64 (NW i + w) + lane (16 bytes
     // each) of a tile; the lane loads the logical piece that the swizzled
@@ -473,11 +477,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
         step(P2{}, c + 2, s_a, s_b, p_b, p_a);
         step(P3{}, c + 3, s_b, s_a, p_a, p_b);
     }
-    if (c < n_chunks) {  // n_chunks is even
-        step(P0{}, c, s_a, s_b, p_b, p_a);
-        step(P1{}, c + 1, s_b, s_a, p_a, p_b);
-    }
-    pv(n_chunks - 1, p_b);
+    // the last 1-3 chunks; P of the last chunk ends in p_a after an even
+    // chunk count's odd step and in p_b after an even step
+    const int rem = n_chunks - c;
+    if (rem >= 1) step(P0{}, c, s_a, s_b, p_b, p_a);
+    if (rem >= 2) step(P1{}, c + 1, s_b, s_a, p_a, p_b);
+    if (rem >= 3) step(P2{}, c + 2, s_a, s_b, p_b, p_a);
+    if (rem & 1) pv(n_chunks - 1, p_a);
+    else pv(n_chunks - 1, p_b);
 #ifdef PELICA_PTRACE
     if (lane == 0) {
         const int wid = blockIdx.x * NW + wave;
