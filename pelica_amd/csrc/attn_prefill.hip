@@ -69,6 +69,13 @@ __device__ __forceinline__ int v_slot(int k, int p) {
 
 // waves per SIMD: 2 (64 query rows per wave at hd 64, 32 at hd 128), or 1
 // with 128 rows per wave (the whole register file for one wave)
+// build switch: streaming tiles for every launch (comparison builds)
+#ifdef PELICA_PRE_NO_RESIDENT
+constexpr bool kNoResidentTiles = true;
+#else
+constexpr bool kNoResidentTiles = false;
+#endif
+
 template <int HD, int RT>
 constexpr int kPrefillOcc = HD * RT >= 256 ? 1 : 2;
 
@@ -81,14 +88,21 @@ __device__ unsigned long long g_ptrace[1 << 17];
 __device__ __forceinline__ unsigned cyc() { return (unsigned)__builtin_amdgcn_s_memtime(); }
 #endif
 
-template <int HD, int RT, bool RING, bool ROUND, int NW>
+// Short key ranges (sliding windows): with NRES > 0 every K and V tile of
+// the workgroup's range (at most NRES of each) is requested at the start and
+// stays resident in LDS, so the chunk loop has no tile waits and no
+// barriers; otherwise tiles stream through two K and two V buffers.
+template <int HD, int RT, bool RING, bool ROUND, int NW, int NRES = 0>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefillOcc<HD, RT>, kPrefillOcc<HD, RT>))) void prefill_kernel(
     PrefillParams p, int n_tb, int TB) {
     constexpr int KS = HD / 16;                 // 16-dim k-steps of QK^T
     constexpr int DT = HD / 32;                 // 32-dim output tiles
     constexpr int TILE = 64 * HD * 2;           // bytes of a 64-key K (or V) tile
     constexpr int PPR = HD / 8;                 // 16-byte pieces per key row
-    __shared__ __attribute__((aligned(16))) char lds[4 * TILE];  // K0 K1 V0 V1
+    // streaming: K0 K1 V0 V1; resident: K[NRES] V[NRES] and a zero tile
+    constexpr int NBUF = NRES ? 2 * NRES + 1 : 4;
+    static_assert(!NRES || !ROUND, "resident tiles: whole-cache launches only");
+    __shared__ __attribute__((aligned(16))) char lds[NBUF * TILE];
 
     // XCD-aware block order: dispatch goes round-robin over the 8 XCDs, so
     // give each XCD a contiguous range of logical blocks (same kv head)
@@ -134,8 +148,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
     // layout puts in its slot.
     constexpr int WI = PPR / NW;  // wave instructions per tile and wave
     static_assert(PPR % NW == 0, "tile pieces must split evenly over the waves");
-    char* const kbuf = lds;              // K tiles: kbuf + (tile & 1) * TILE
-    char* const vbuf = lds + 2 * TILE;   // V tiles: vbuf + (tile & 1) * TILE
+    char* const kbuf = lds;                            // K tiles
+    char* const vbuf = lds + (NRES ? NRES : 2) * TILE;  // V tiles
+    // buffer of tile t: its own (resident) or t & 1 (streaming)
+    auto tbuf = [](int t) { return NRES ? t : (t & 1); };
     auto load_tile = [&](const __amdgpu_buffer_rsrc_t& rs, char* dst, int tile, bool is_v) {
         const int kb = kb0 + 64 * tile;
 #pragma unroll
@@ -204,7 +220,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
     // S^T of chunk c (32 keys x RT row tiles): element i of a lane is key
     // 32 c + 8 (i / 4) + 4 h2 + i % 4 of row c32
     auto qk = [&](int c, float16v (&sc)[RT]) {
-        const char* kt = kbuf + ((c >> 1) & 1) * TILE;
+        const char* kt = kbuf + tbuf(c >> 1) * TILE;
         const int krow = 32 * (c & 1) + c32;
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) sc[rt] = float16v{};
@@ -217,7 +233,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
     };
     // O^T += V^T P^T over chunk c; pb[w] holds keys 16 w .. 16 w + 15 of it
     auto pv = [&](int c, const half8 (&pb)[2][RT]) {
-        const char* vt = vbuf + ((c >> 1) & 1) * TILE;
+        const char* vt = vbuf + tbuf(c >> 1) * TILE;
         const int G = lane >> 4, r4 = (lane & 15) >> 2, q4 = lane & 3;
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
@@ -252,15 +268,23 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
     // maximum far above m) the wave takes the exact path: chunk max, rescale
     // O and l, recompute P.
     constexpr float kSumLimit = 16384.f;
+    // the (empty) PV of chunk -1 reads this zeroed tile: V tile 1's
+    // buffer (streaming) or the tile after the resident ones
+    char* const vzero = NRES ? lds + 2 * NRES * TILE : vbuf + TILE;
     if (n_tiles > 0) {  // (uniform over the workgroup)
     {
-        // V tile 1's buffer feeds the (empty) PV of chunk -1: zero it
 #pragma unroll
         for (int i = 0; i < TILE / (16 * 64 * NW); ++i)
-            *reinterpret_cast<u32x4*>(vbuf + TILE + 16 * (tid + 64 * NW * i)) = u32x4{0, 0, 0, 0};
-        load_tile(rk, kbuf, 0, false);
-        if (n_tiles > 1) load_tile(rk, kbuf + TILE, 1, false);
-        load_tile(rv, vbuf, 0, true);
+            *reinterpret_cast<u32x4*>(vzero + 16 * (tid + 64 * NW * i)) = u32x4{0, 0, 0, 0};
+        if (NRES) {
+            // (the launch guarantees n_tiles <= NRES)
+            for (int t = 0; t < n_tiles; ++t) load_tile(rk, kbuf + t * TILE, t, false);
+            for (int t = 0; t < n_tiles; ++t) load_tile(rv, vbuf + t * TILE, t, true);
+        } else {
+            load_tile(rk, kbuf, 0, false);
+            if (n_tiles > 1) load_tile(rk, kbuf + TILE, 1, false);
+            load_tile(rv, vbuf, 0, true);
+        }
         wait_tiles();
     }
     __syncthreads();
@@ -288,7 +312,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
         // K of tile t+2 and V of tile t+1 at odd chunks c = 2t+1: their
         // buffers' last readers finished at chunk 2t; first readers at 2t+3
         const int t = c >> 1;
-        if (PAR & 1) {
+        if (!NRES && (PAR & 1)) {
             if (t + 2 < n_tiles) load_tile(rk, kbuf + (t & 1) * TILE, t + 2, false);
             if (t + 1 < n_tiles) load_tile(rv, vbuf + ((t + 1) & 1) * TILE, t + 1, true);
         }
@@ -310,9 +334,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
         // operands ahead of its first MFMA
         constexpr int NOPD = KS + 2 * DT;
         half8 opd[NOPD];
-        const char* const kt_c = kbuf + (((PAR + 1) >> 1) & 1) * TILE;
+        // (resident tiles: PAR = c itself)
+        const char* const kt_c = kbuf + (NRES ? ((PAR + 1) >> 1) : (((PAR + 1) >> 1) & 1)) * TILE;
         const int krow = 32 * ((PAR + 1) & 1) + c32;
-        const char* const vt_c = vbuf + (((PAR + 3) >> 1) & 1) * TILE;  // chunk c-1 (c = 0: the zeroed tile 1)
+        // chunk c-1 (c = 0: the zeroed tile)
+        const char* const vt_c = NRES ? (PAR == 0 ? vzero : vbuf + ((PAR - 1) >> 1) * TILE)
+                                      : vbuf + (((PAR + 3) >> 1) & 1) * TILE;
         auto read_opd = [&](int r) {
             if (r < KS) {
                 opd[r] = *reinterpret_cast<const half8*>(kt_c + k_slot<HD>(krow, 2 * r + h2));
@@ -446,7 +473,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
         // chunk 2t, and (b) the loads of chunk 2t-1 are first read at chunk
         // 2t+1, so they must have landed (vmcnt(0)) before it.  Chunk 2t+1
         // reads only tiles published by this barrier or earlier ones.
-        if ((PAR & 1) == 0) {
+        if (!NRES && (PAR & 1) == 0) {
 #ifdef PELICA_PTRACE
             const unsigned ta = cyc();
             wait_tiles();
@@ -470,6 +497,25 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
     using P1 = std::integral_constant<int, 1>;
     using P2 = std::integral_constant<int, 2>;
     using P3 = std::integral_constant<int, 3>;
+    if constexpr (NRES > 0) {
+        // every chunk unrolled (n_chunks <= 2 NRES); PAR = c
+        static_assert(NRES <= 4, "unrolled chunk steps");
+        using P4 = std::integral_constant<int, 4>;
+        using P5 = std::integral_constant<int, 5>;
+        using P6 = std::integral_constant<int, 6>;
+        using P7 = std::integral_constant<int, 7>;
+        step(P0{}, 0, s_a, s_b, p_b, p_a);
+        if (n_chunks > 1) step(P1{}, 1, s_b, s_a, p_a, p_b);
+        if (n_chunks > 2) step(P2{}, 2, s_a, s_b, p_b, p_a);
+        if (n_chunks > 3) step(P3{}, 3, s_b, s_a, p_a, p_b);
+        if (NRES > 2 && n_chunks > 4) step(P4{}, 4, s_a, s_b, p_b, p_a);
+        if (NRES > 2 && n_chunks > 5) step(P5{}, 5, s_b, s_a, p_a, p_b);
+        if (NRES > 3 && n_chunks > 6) step(P6{}, 6, s_a, s_b, p_b, p_a);
+        if (NRES > 3 && n_chunks > 7) step(P7{}, 7, s_b, s_a, p_a, p_b);
+        // P of the last chunk: p_a after an even chunk, p_b after an odd one
+        if (n_chunks & 1) pv(n_chunks - 1, p_a);
+        else pv(n_chunks - 1, p_b);
+    } else {
     int c = 0;
     for (; c + 4 <= n_chunks; c += 4) {
         step(P0{}, c, s_a, s_b, p_b, p_a);
@@ -485,6 +531,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
     if (rem >= 3) step(P2{}, c + 2, s_a, s_b, p_b, p_a);
     if (rem & 1) pv(n_chunks - 1, p_a);
     else pv(n_chunks - 1, p_b);
+    }
 #ifdef PELICA_PTRACE
     if (lane == 0) {
         const int wid = blockIdx.x * NW + wave;
@@ -537,6 +584,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
     }
 }
 
+// 64-key tiles a token block of TB tokens can need under a window: keys
+// [pos_first + 1 - window, pos_last] from a 32-aligned start (0: no bound)
+static int window_tiles(int window, int TB) {
+    if (window <= 0) return 0;
+    const int chunks = (TB - 1 + window - 1 + 31) / 32 + 1;
+    return (chunks + 1) / 2;
+}
+
 template <int HD, int RT, int NW>
 static hipError_t launch_nw(const PrefillParams& p, hipStream_t st) {
     constexpr int ROWS = NW * RT * 32;
@@ -546,12 +601,24 @@ static hipError_t launch_nw(const PrefillParams& p, hipStream_t st) {
     const long long nblk = (long long)n_tb * p.n_kv * p.n_seq;
     if (nblk > 0x7fffffff) return hipErrorNotSupported;
     ProfScope ps(kProfPrefill, st);
+    const dim3 grid((unsigned)nblk), block(64 * NW);
+    // head dim 64: short windows keep all their K/V tiles in LDS (<= 3 of
+    // each: 56 KB, two 4-wave workgroups per CU)
+    const int wt = window_tiles(p.window, TB);
+    const bool res = HD == 64 && !p.state && wt > 0 && wt <= 3 && !kNoResidentTiles;
+    if constexpr (HD == 64 && NW == 4) {
+        if (res) {
+            if (p.ring_cap) hipLaunchKernelGGL((prefill_kernel<HD, RT, true, false, NW, 3>), grid, block, 0, st, p, n_tb, TB);
+            else hipLaunchKernelGGL((prefill_kernel<HD, RT, false, false, NW, 3>), grid, block, 0, st, p, n_tb, TB);
+            return hipGetLastError();
+        }
+    }
     if (p.state)
-        hipLaunchKernelGGL((prefill_kernel<HD, RT, false, true, NW>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p, n_tb, TB);
+        hipLaunchKernelGGL((prefill_kernel<HD, RT, false, true, NW>), grid, block, 0, st, p, n_tb, TB);
     else if (p.ring_cap)
-        hipLaunchKernelGGL((prefill_kernel<HD, RT, true, false, NW>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p, n_tb, TB);
+        hipLaunchKernelGGL((prefill_kernel<HD, RT, true, false, NW>), grid, block, 0, st, p, n_tb, TB);
     else
-        hipLaunchKernelGGL((prefill_kernel<HD, RT, false, false, NW>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p, n_tb, TB);
+        hipLaunchKernelGGL((prefill_kernel<HD, RT, false, false, NW>), grid, block, 0, st, p, n_tb, TB);
     return hipGetLastError();
 }
 

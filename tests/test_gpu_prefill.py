@@ -42,7 +42,7 @@ def test_small_prompts(T, hd, n_head, n_kv):
 
 
 @pytest.mark.parametrize("window", [1, 17, 64, 128, 1000])
-@pytest.mark.parametrize("hd,n_head,n_kv", [(64, 64, 8), (128, 32, 4)])
+@pytest.mark.parametrize("hd,n_head,n_kv", [(64, 64, 8), (128, 32, 4), (64, 16, 4)])
 def test_windows(window, hd, n_head, n_kv):
     cfg = wl.AttnConfig("pw", "prefill", n_head, n_kv, hd, 700, q_tokens=700, window=window, sinks=True,
                         seed=window + hd)
