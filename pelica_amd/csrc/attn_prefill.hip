@@ -81,11 +81,14 @@ constexpr int kPrefillOcc = HD * RT >= 256 ? 1 : 2;
 
 // Build-time instrumentation (off by default; -DPELICA_PTRACE): per wave,
 // shader-clock cycles spent in the tile loop, waiting for tile loads and at
-// the per-chunk barrier, and the number of exact-path chunks, stored in
-// g_ptrace[wave * 4 + k]; pelica_attn_debug_ptrace() copies them out.
+// the per-chunk barrier, the number of exact-path chunks, and 100 MHz
+// real-time stamps at entry, loop start, loop end and exit (their ratio to
+// the cycle count gives the shader clock), stored in g_ptrace[wave * 8 + k];
+// pelica_attn_debug_ptrace() copies them out.
 #ifdef PELICA_PTRACE
-__device__ unsigned long long g_ptrace[1 << 17];
+__device__ unsigned long long g_ptrace[1 << 18];
 __device__ __forceinline__ unsigned cyc() { return (unsigned)__builtin_amdgcn_s_memtime(); }
+__device__ __forceinline__ unsigned long long rtime() { return __builtin_amdgcn_s_memrealtime(); }
 #endif
 
 // Short key ranges (sliding windows): with NRES > 0 every K and V tile of
@@ -102,7 +105,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
     // streaming: K0 K1 V0 V1; resident: K[NRES] V[NRES] and a zero tile
     constexpr int NBUF = NRES ? 2 * NRES + 1 : 4;
     static_assert(!NRES || !ROUND, "resident tiles: whole-cache launches only");
-    __shared__ __attribute__((aligned(16))) char lds[NBUF * TILE];
+    // after the tile loop the f16 output of each wave is staged here
+    constexpr int OUT_WAVE = RT * 32 * HD * 2;  // bytes of one wave's output rows
+    constexpr int LDS_BYTES = (ROUND || NBUF * TILE >= NW * OUT_WAVE) ? NBUF * TILE : NW * OUT_WAVE;
+    __shared__ __attribute__((aligned(16))) char lds[LDS_BYTES];
 
     // XCD-aware block order: dispatch goes round-robin over the 8 XCDs, so
     // give each XCD a contiguous range of logical blocks (same kv head)
@@ -114,6 +120,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
     const int kvh = rest % p.n_kv, s = rest / p.n_kv;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h2 = lane >> 5, c32 = lane & 31;
+#ifdef PELICA_PTRACE
+    const unsigned long long rt_entry = rtime();
+    unsigned long long rt_loop0 = 0, rt_loop1 = 0;
+#endif
     const int len = seq_keys(p.seq_len, s, p.kv_len);
     if (len < p.T || len <= 0) return;
     const int64_t row0 = p.seq_off ? p.seq_off[s] : (int64_t)s * (p.ring_cap ? p.ring_cap : p.kv_len);
@@ -492,6 +502,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
     };
 #ifdef PELICA_PTRACE
     const unsigned t_start = cyc();
+    rt_loop0 = rtime();
 #endif
     using P0 = std::integral_constant<int, 0>;
     using P1 = std::integral_constant<int, 1>;
@@ -533,16 +544,54 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
     else pv(n_chunks - 1, p_b);
     }
 #ifdef PELICA_PTRACE
+    rt_loop1 = rtime();
     if (lane == 0) {
         const int wid = blockIdx.x * NW + wave;
-        g_ptrace[wid * 4 + 0] = cyc() - t_start;
-        g_ptrace[wid * 4 + 1] = t_wait;
-        g_ptrace[wid * 4 + 2] = t_bar;
-        g_ptrace[wid * 4 + 3] = (unsigned long long)n_exact << 32 | (unsigned)n_chunks;
+        g_ptrace[wid * 8 + 0] = cyc() - t_start;
+        g_ptrace[wid * 8 + 1] = t_wait;
+        g_ptrace[wid * 8 + 2] = t_bar;
+        g_ptrace[wid * 8 + 3] = (unsigned long long)n_exact << 32 | (unsigned)n_chunks;
     }
 #endif
     }
 
+    if constexpr (!ROUND) {
+        // Output through LDS: each wave writes its rows (normalised, f16)
+        // into its own area, then stores whole rows — consecutive rows are
+        // consecutive heads of a token, so one store instruction writes
+        // 512 B (hd 64) of contiguous output instead of 16-byte pieces of
+        // 32 rows.  Rows of 16-byte pieces, piece p of local row r at slot
+        // p ^ (r % PPR).
+        __syncthreads();  // every wave is done with the K/V tiles
+        char* const ow = lds + wave * OUT_WAVE;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            const float inv = 1.f / half_sum(l[rt]);
+            const int rl = rt * 32 + c32;
+            // O^T lane layout: dim 32 dt + 8 (i / 4) + 4 h2 + i % 4 of row c32
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    const half4 hv = {(_Float16)(o[dt][rt][4 * i4] * inv), (_Float16)(o[dt][rt][4 * i4 + 1] * inv),
+                                      (_Float16)(o[dt][rt][4 * i4 + 2] * inv), (_Float16)(o[dt][rt][4 * i4 + 3] * inv)};
+                    const int pc = 4 * dt + i4;
+                    *reinterpret_cast<half4*>(ow + rl * (HD * 2) + ((pc ^ (rl % PPR)) << 4) + 8 * h2) = hv;
+                }
+        }
+        // (a wave's LDS accesses complete in order: it reads its own rows)
+        constexpr int RPI = 64 / PPR;  // rows per store instruction
+        const int pc = lane % PPR;
+#pragma unroll
+        for (int k = 0; k < RT * 32 / RPI; ++k) {
+            const int rl = k * RPI + lane / PPR;
+            const u32x4 val = *reinterpret_cast<const u32x4*>(ow + rl * (HD * 2) + ((pc ^ (rl % PPR)) << 4));
+            const int r = wave * RT * 32 + rl;
+            const int t = t0 + r / p.hpk, h = kvh * p.hpk + r % p.hpk;
+            if (r < TB * p.hpk && t < t1)
+                *reinterpret_cast<u32x4*>(p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + 8 * pc) = val;
+        }
+    } else {
     // O^T lane layout: dim 32 dt + 8 (i / 4) + 4 h2 + i % 4 of row c32
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
@@ -582,6 +631,17 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
                 *reinterpret_cast<half4*>(op + 32 * dt + 8 * i4) = hv;
             }
     }
+    }
+#ifdef PELICA_PTRACE
+    // (stores issued; the wave ends when they are done)
+    if (lane == 0) {
+        const int wid = blockIdx.x * NW + wave;
+        g_ptrace[wid * 8 + 4] = rt_entry;
+        g_ptrace[wid * 8 + 5] = rt_loop0;
+        g_ptrace[wid * 8 + 6] = rt_loop1;
+        g_ptrace[wid * 8 + 7] = rtime();
+    }
+#endif
 }
 
 // 64-key tiles a token block of TB tokens can need under a window: keys
