@@ -66,9 +66,11 @@ def test_ragged_sequences():
     assert_close(as_f64(gpu_run(inp)), as_f64(oracle_run(inp)), what="ragged")
 
 
-@pytest.mark.parametrize("hd,n_head,n_kv", [(64, 64, 8), (128, 32, 4)])
-def test_ring_window_prefill(hd, n_head, n_kv):
-    cap, L, T, W = 128 + 512, 3000, 512, 128
+@pytest.mark.parametrize("hd,n_head,n_kv,T", [(64, 64, 8, 512), (128, 32, 4, 512), (64, 64, 8, 4096)])
+def test_ring_window_prefill(hd, n_head, n_kv, T):
+    # (4096 tokens at head dim 64: two token blocks per workgroup over
+    # resident tiles; 512: one)
+    cap, L, W = 128 + T, T + 2488, 128
     cfg = wl.AttnConfig("pring", "prefill", n_head, n_kv, hd, L, q_tokens=T, window=W, sinks=True, seed=73 + hd)
     inp = wl.make_inputs(cfg, "cuda")
     kr = torch.zeros(cap, n_kv, hd, dtype=torch.float16, device="cuda")
@@ -76,7 +78,7 @@ def test_ring_window_prefill(hd, n_head, n_kv):
     idx = torch.arange(L - cap, L, device="cuda")
     kr[idx % cap] = inp.k[idx]
     vr[idx % cap] = inp.v[idx]
-    print(f"[case] prefill ring hd{hd}", flush=True)
+    print(f"[case] prefill ring hd{hd} T{T}", flush=True)
     got = gpu_run(inp, ring_cap=cap, k=kr, v=vr)
     assert_close(as_f64(got), as_f64(oracle_run(inp)), what=f"prefill ring hd{hd}")
 
