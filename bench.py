@@ -326,6 +326,14 @@ def profile_only(args):
     from pelica_amd import workloads as wl
 
     for name in args.profile.split(","):
+        if name == "mla_decode_h32_32k":  # MLA decode over rotating latent copies
+            g = torch.Generator(device="cuda").manual_seed(12)
+            q = torch.randn(1, 1, 32, 512, generator=g, device="cuda") * 0.25
+            lats = rotating_copies((torch.randn(32768, 512, generator=g, device="cuda") * 0.5).half())
+            for i in range(args.steps):
+                attn.mla(q, lats[i % len(lats)], kv_len=32768)
+            torch.cuda.synchronize()
+            continue
         if name == "copy":  # calibration: a plain 256 MiB device copy
             x = torch.ones(256 << 20, dtype=torch.uint8, device="cuda")
             y = torch.empty_like(x)
