@@ -652,6 +652,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     // are done (lgkmcnt): K(i+1) after QK^T, V(i+1) after PV.  (Loads past
     // the wave's last block are not issued, so nothing is pending when the
     // state reuses the buffers.)
+    // The vmcnt waits below are counted by hand from that order (VPL loads
+    // per K or V block): the loop body, qk() and softmax_pv() must issue no
+    // other vector-memory operation (no global or buffer load or store), or
+    // a wait would return before its block has landed.
     for (int i = 0; i < nb; ++i) {
         wait_vm<VPL>();  // K(i) landed
         if (i == 0) DTRACE(1);
