@@ -57,14 +57,36 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(QkvParams p) {
 
     float4v x = live ? load4<VEC>(src + e0) : float4v{0.f, 0.f, 0.f, 0.f};
 
-    // per-head RMS norm: the sum of squares over the head's LPH lanes
+    // the norm weights and the rotation's (cos, sin) of this lane's elements
+    // are requested with the row, not after it
     const float* w = kind == 0 ? p.q_norm : kind == 1 ? p.k_norm : nullptr;
+    const float4v wv = w ? load4<false>(w + e0) : float4v{1.f, 1.f, 1.f, 1.f};
+    const bool rot = kind < 2 && p.table && e0 < p.rot;
+    float2 cssn[4];
+    if (rot) {
+        const int half = p.rot / 2;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = e0 + i;
+            const int j = e >= p.rot ? 0 : p.neox ? (e < half ? e : e - half) : e >> 1;
+            if (p.table_split <= 0) {
+                cssn[i] = *reinterpret_cast<const float2*>(p.table + ((size_t)pos * half + j) * 2);
+            } else {
+                // angle addition of the rows for pos / 256 and pos % 256
+                const float2 c1 = *reinterpret_cast<const float2*>(p.table + ((size_t)(pos >> 8) * half + j) * 2);
+                const float2 c2 =
+                    *reinterpret_cast<const float2*>(p.table + ((size_t)(p.table_split + (pos & 255)) * half + j) * 2);
+                cssn[i] = make_float2(c1.x * c2.x - c1.y * c2.y, c1.y * c2.x + c1.x * c2.y);
+            }
+        }
+    }
+
+    // per-head RMS norm: the sum of squares over the head's LPH lanes
     float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
 #pragma unroll
     for (int off = LPH / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
     if (w) {
         const float inv = 1.f / __builtin_sqrtf(ss / (float)HD + p.eps);
-        const float4v wv = load4<false>(w + e0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) x[i] = x[i] * inv * wv[i];
     }
@@ -77,38 +99,23 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(QkvParams p) {
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    if (kind < 2 && p.table && e0 < p.rot) {
+    if (rot) {
         const float* r = row[wave][sub];
         const int half = p.rot / 2;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int e = e0 + i;
             if (e >= p.rot) continue;
-            int j, a, b;
+            int a, b;
             if (p.neox) {
-                j = e < half ? e : e - half;
-                a = j;
-                b = j + half;
+                a = e < half ? e : e - half;
+                b = a + half;
             } else {
-                j = e >> 1;
-                a = 2 * j;
-                b = 2 * j + 1;
-            }
-            float cs, sn;
-            if (p.table_split <= 0) {
-                const float2 c = *reinterpret_cast<const float2*>(p.table + ((size_t)pos * half + j) * 2);
-                cs = c.x;
-                sn = c.y;
-            } else {
-                // angle addition of the rows for pos / 256 and pos % 256
-                const float2 c1 = *reinterpret_cast<const float2*>(p.table + ((size_t)(pos >> 8) * half + j) * 2);
-                const float2 c2 =
-                    *reinterpret_cast<const float2*>(p.table + ((size_t)(p.table_split + (pos & 255)) * half + j) * 2);
-                cs = c1.x * c2.x - c1.y * c2.y;
-                sn = c1.y * c2.x + c1.x * c2.y;
+                a = e & ~1;
+                b = a + 1;
             }
             const float x0 = r[a], x1 = r[b];
-            x[i] = e == a ? x0 * cs - x1 * sn : x0 * sn + x1 * cs;
+            x[i] = e == a ? x0 * cssn[i].x - x1 * cssn[i].y : x0 * cssn[i].y + x1 * cssn[i].x;
         }
     }
     if (!live) return;
