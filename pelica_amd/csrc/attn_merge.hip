@@ -2,8 +2,11 @@
 // format: {M natural-log max, L, O[hd]} per slot, token and head) into the
 // attention output, with optional sinks.
 //
-// Grid (n_head, n_tokens): one 512-thread workgroup per (token, head), as
-// ATTN_M's grid (n_head, TMAX) (src/oss_batch.rs:395-425).  As merge_dec_fast
+// Grid (n_head x dim slices, n_tokens): 512-thread workgroups per (token,
+// head), as ATTN_M's grid (n_head, TMAX) (src/oss_batch.rs:395-425), each
+// head's dims cut into slices when the grid would be small (every slice
+// reduces the slots' (max, sum) pairs itself: 8 bytes a slot against its
+// dw * 4 of O).  As merge_dec_fast
 // does (src/moe_kernels.rs:750-808), each slot's weight e^(M_c - M) is
 // computed once, by one thread, into LDS (tiles of kTile slots); then thread
 // (phase, dim pair) sums its phase's slots c = phase (mod phases) with those
@@ -39,21 +42,22 @@ __device__ __forceinline__ float block_reduce(float x, float* red, bool is_max) 
     return r;
 }
 
-__global__ __launch_bounds__(kThreads) void partials_merge_kernel(int n_tok, int n_head, int hd, int n_parts,
+__global__ __launch_bounds__(kThreads) void partials_merge_kernel(int n_tok, int n_head, int hd, int dw, int n_parts,
                                                                   const float* __restrict__ parts,
                                                                   const float* __restrict__ sinks,
                                                                   float* __restrict__ out) {
     __shared__ float2 ml_s[kTile];   // this tile's (max, sum) pairs, then (weight, -)
     __shared__ float red[kThreads / 64];
     __shared__ float2 acc_s[kThreads];
-    const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    const int nds = hd / dw;  // dim slices per head
+    const int h = blockIdx.x / nds, d0 = dw * (blockIdx.x % nds), t = blockIdx.y, tid = threadIdx.x;
     const size_t stride = (size_t)n_tok * n_head * (hd + 2);  // floats between slots
     const float* ph = parts + ((size_t)t * n_head + h) * (hd + 2);
-    const int dp_n = hd / 2;                   // dim pairs (hd <= 1024: <= 512)
+    const int dp_n = dw / 2;                   // dim pairs of the slice (dw <= 1024: <= 512)
     const int n_ph = kThreads / dp_n;          // slot phases
     const int ph_i = tid / dp_n, dp = tid % dp_n;
     const bool worker = ph_i < n_ph;
-    const float* po = ph + 2 + 2 * dp;
+    const float* po = ph + 2 + d0 + 2 * dp;
     const float sk = sinks ? sinks[h] : -INFINITY;
 
     // the largest max (natural log) over every slot and the sink
@@ -118,7 +122,7 @@ __global__ __launch_bounds__(kThreads) void partials_merge_kernel(int n_tok, int
             r.y += y.y;
         }
         const float inv = 1.f / L;
-        *reinterpret_cast<float2*>(out + ((size_t)t * n_head + h) * hd + 2 * tid) = make_float2(r.x * inv, r.y * inv);
+        *reinterpret_cast<float2*>(out + ((size_t)t * n_head + h) * hd + d0 + 2 * tid) = make_float2(r.x * inv, r.y * inv);
     }
 }
 
@@ -127,9 +131,14 @@ __global__ __launch_bounds__(kThreads) void partials_merge_kernel(int n_tok, int
 hipError_t launch_partials_merge(int n_tok, int n_head, int hd, int n_parts, const float* parts, const float* sinks,
                                  float* out, hipStream_t st) {
     if (hd <= 0 || hd % 2 || hd > 2 * kThreads) return hipErrorInvalidValue;
+    // dim slices: halve the slice (down to 32 dims, even, dividing hd) while
+    // the grid is below 128 workgroups (one token of 32 heads: 11.2 -> 9.2
+    // us; four tokens, already 128 workgroups: slicing further cost 6 %)
+    int dw = hd;
+    while ((long long)n_head * n_tok * (hd / dw) < 128 && dw % 4 == 0 && dw / 2 >= 32) dw /= 2;
     ProfScope ps(kProfMerge, st);
-    hipLaunchKernelGGL(partials_merge_kernel, dim3(n_head, n_tok), dim3(kThreads), 0, st, n_tok, n_head, hd, n_parts,
-                       parts, sinks, out);
+    hipLaunchKernelGGL(partials_merge_kernel, dim3(n_head * (hd / dw), n_tok), dim3(kThreads), 0, st, n_tok, n_head, hd,
+                       dw, n_parts, parts, sinks, out);
     return hipGetLastError();
 }
 
