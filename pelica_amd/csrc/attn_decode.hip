@@ -857,18 +857,22 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
 // threads; thread (phase, 4-dim chunk) merges the splits c = phase (mod
 // phases) online (running max, rescaled sum), all of its loads in flight
 // at once; the phases of a wave merge through lane exchanges, the four
-// waves through LDS, in a fixed order.  ROW_WAVES: one wave per row (four
-// rows per workgroup, grid x = R / 4), for rows with few splits (<= 16):
-// no LDS stage, a quarter of the workgroups.
+// waves through LDS, in a fixed order; head dim 128 takes four workgroups
+// per row (32 dims each).  ROW_WAVES: one wave per row (four rows per
+// workgroup, grid x = R / 4), for rows with few splits (<= 16): no LDS
+// stage, a quarter of the workgroups.
 template <int HD, bool ROW_WAVES>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
     static_assert(!ROW_WAVES || HD <= 128, "one wave covers the row's dims");
-    constexpr int DW = HD < 128 ? HD : 128;  // dims per workgroup (hd 512: four workgroups per row)
+    // dims per workgroup: hd 128 in four slices of 32 (calls of C2's size
+    // have only rows x kv heads = 32 rows: four times the workgroups load
+    // the partials, 11.5 -> 11.3 us), hd 512 in four of 128
+    constexpr int DW = (HD == 128 && !ROW_WAVES) ? 32 : HD < 128 ? HD : 128;
     constexpr int NQ = HD / DW;
     constexpr int D4 = DW / 4;
-    // phases: 16 (hd 64), 8 (hd 128 and 512); one wave per row: 4, 2
+    // phases: 16 (hd 64), 32 (hd 128), 8 (hd 512); one wave per row: 4, 2
     constexpr int PH = (ROW_WAVES ? 64 : 256) / D4;
-    constexpr int J = 8;                // splits per thread per pass
+    constexpr int J = DW < 128 && HD == 128 ? 4 : 8;  // splits per thread per pass
     __shared__ float4v s_o[4][D4];
     __shared__ float2 s_ml[4][D4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -941,6 +945,11 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
     // Exchange with lane ^ off (off = 16 or 32) by permlane swaps (no LDS):
     // each lane gets the pair (value of the lower lane, value of the upper).
     auto pair = [](float x, int off) {
+        if (off < 16) {  // (the lane off apart, through the LDS crossbar)
+            const float y = __shfl_xor(x, off, 64);
+            const bool upper = (threadIdx.x & off) != 0;
+            return upper ? make_float2(y, x) : make_float2(x, y);
+        }
         const auto v = off == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false)
                                  : __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
         return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
@@ -1036,7 +1045,7 @@ hipError_t launch_combine(const DecodeParams& p, hipStream_t st) {
         else hipLaunchKernelGGL((decode_combine_kernel<128, true>), grid, dim3(256), 0, st, p);
         return hipGetLastError();
     }
-    const dim3 grid(p.R * (p.hd > 128 ? p.hd / 128 : 1), p.n_kv, p.n_seq);
+    const dim3 grid(p.R * (p.hd > 128 ? p.hd / 128 : p.hd == 128 ? 4 : 1), p.n_kv, p.n_seq);
     switch (p.hd) {
         case 64: hipLaunchKernelGGL((decode_combine_kernel<64, false>), grid, dim3(256), 0, st, p); break;
         case 128: hipLaunchKernelGGL((decode_combine_kernel<128, false>), grid, dim3(256), 0, st, p); break;
