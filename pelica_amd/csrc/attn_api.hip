@@ -251,17 +251,25 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl, bool allow_fuse = true)
     return PELICA_ATTN_OK;
 }
 
-// MLA: rows = tokens x heads in row groups of 16 RT; 32-key blocks split so
-// ~one workgroup per CU streams the latent (one workgroup fills a CU's LDS)
+// MLA: rows = tokens x heads in row groups of 16, 32-key latent blocks.
+// Measured on MI355X (32K-128K latent rows, 16-4096 rows): two workgroups
+// per CU (512) is fastest while that leaves each workgroup >= 8 blocks,
+// else one per CU (256); a split shorter than 128 keys loses more to its
+// partials (2 KB a row) than it gains.
 int plan_mla(const PelicaAttnDesc* d, DecodePlan* pl) {
     int rc = check_desc(d, true);
     if (rc) return rc;
     const int R = d->q_tokens * d->n_head;
-    const int rt = R <= 16 ? 1 : R <= 32 ? 2 : 4;
+    const int rt = 1;
     const int n_rg = ceil_div(R, 16 * rt);
     const long long blocks = (long long)ceil_div(d->kv_len, 32) * n_rg * d->n_seq;
-    const int target = tuning().mla_workgroups ? tuning().mla_workgroups : 256;
-    long long split_keys = 32LL * std::max<long long>(1, (blocks + target - 1) / target);
+    long long split_keys;
+    if (tuning().mla_workgroups) {
+        split_keys = 32LL * std::max<long long>(1, ceil_div(blocks, tuning().mla_workgroups));
+    } else {
+        const long long target = blocks >= 8 * 512 ? 512 : 256;
+        split_keys = std::max<long long>(128, 32LL * ceil_div(blocks, target));
+    }
     int n_slot = ceil_div(d->kv_len, split_keys);
     while (n_slot > pelica::kMaxSlots) {
         split_keys *= 2;
@@ -594,7 +602,8 @@ int pelica_attn_mla(const PelicaAttnDesc* desc, const float* q, const uint16_t* 
     p.n_slot = pl.n_slot;
     p.split_keys = pl.split_keys;
     p.wg_heads = 1;
-    hipError_t e = pelica::launch_mla(p, pl.rt, static_cast<hipStream_t>(stream));
+    p.rg_rows = 16 * pl.rt;
+    hipError_t e = pelica::launch_mla(p, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(PELICA_ATTN_EHIP, "mla launch: %s", hipGetErrorString(e));
     return PELICA_ATTN_OK;
 }

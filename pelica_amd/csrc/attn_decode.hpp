@@ -58,7 +58,7 @@ hipError_t launch_decode(const DecodeParams& p, int rt, int nw, hipStream_t st);
 // the in-order combine of the split partials in p.ws_ml / p.ws_o (hd 64, 128, 512)
 hipError_t launch_combine(const DecodeParams& p, hipStream_t st);
 // MLA: n_kv = 1, K = V = latent rows of 512, rows = tokens x heads (attn_mla.hip)
-hipError_t launch_mla(const DecodeParams& p, int rt, hipStream_t st);
+hipError_t launch_mla(const DecodeParams& p, hipStream_t st);
 // zero n counters with a fill kernel (graph-capturable)
 hipError_t launch_zero(unsigned* p, size_t n, hipStream_t st);
 

@@ -4,10 +4,12 @@
 // src/gpu.rs:262-307 (called from src/forward.rs:936-960), as split-K
 // flash-decode with an in-order combine.
 //
-// Work split.  A workgroup of 4 waves owns (sequence, row group of RT x 16
-// query rows = (token, head) pairs, key split).  Latent blocks of 32 keys
-// (32 KB) go from HBM straight into LDS (buffer_load ... lds, double
-// buffered); K = V, so each block is read from HBM once for both products.
+// Work split.  A workgroup of 4 waves owns (sequence, row group of 16 query
+// rows = (token, head) pairs, key split).  Latent blocks of 32 keys (32 KB)
+// go from HBM straight into LDS (buffer_load ... lds, double buffered: ~74 KB
+// of LDS, so two workgroups share a CU and one's loads and barriers hide
+// behind the other's math); K = V, so each block is read from HBM once for
+// both products (the row groups of a split read it through the same L2).
 // Wave w owns dims [128 w, 128 w + 128): it computes the partial scores
 // S_w^T = K[:, dims] Q[:, dims]^T on v_mfma_f32_16x16x32_f16 (Q split into
 // f16 hi + lo parts, ~fp32 products), the four partials are summed through
@@ -41,7 +43,7 @@ constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >>
 }  // namespace
 
 template <int RT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void mla_kernel(DecodeParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void mla_kernel(DecodeParams p) {
     constexpr int HD = kMlaHd, NW = 4, KB = 32;  // dims, waves, keys per block
     constexpr int DS = HD / NW / 32;             // 32-dim k-steps per wave (4)
     constexpr int DT = HD / NW / 16;             // 16-dim output tiles per wave (8)
@@ -51,7 +53,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #endif
     constexpr int NPP = PELICA_MLA_P_PARTS;  // f16 parts of P (the PV weights)
     constexpr int BLK = KB * HD * 2;             // 32 KB
-    constexpr int NBUF = RT == 4 ? 3 : 4;        // latent blocks in the LDS ring
+    constexpr int NBUF = 2;  // latent blocks in the LDS ring (two workgroups fit a CU's LDS)
     constexpr int LPB = KB / NW;                 // loads per block per thread
     constexpr int PS = KB + 4;  // partial-score row stride in floats: rows land on distinct banks
     __shared__ __attribute__((aligned(16))) char lds[NBUF * BLK + NW * ROWS * PS * 4];
@@ -272,14 +274,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
 }
 
-hipError_t launch_mla(const DecodeParams& p, int rt, hipStream_t st) {
+hipError_t launch_mla(const DecodeParams& p, hipStream_t st) {
+    if (p.rg_rows != 16) return hipErrorInvalidValue;
     const dim3 grid(p.n_slot, p.n_rg, p.n_seq);
     {
         ProfScope ps(kProfDecodeSplit, st);
-        if (rt == 1) hipLaunchKernelGGL(mla_kernel<1>, grid, dim3(256), 0, st, p);
-        else if (rt == 2) hipLaunchKernelGGL(mla_kernel<2>, grid, dim3(256), 0, st, p);
-        else if (rt == 4) hipLaunchKernelGGL(mla_kernel<4>, grid, dim3(256), 0, st, p);
-        else return hipErrorInvalidValue;
+        hipLaunchKernelGGL(mla_kernel<1>, grid, dim3(256), 0, st, p);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.n_slot == 1) return e;

@@ -29,7 +29,8 @@ def _oracle(q, lat, L, scale, **kw):
     return orc.attention(qn, ln, ln, n_kv=1, kv_len=L, scale=scale, **kw)
 
 
-@pytest.mark.parametrize("n_head,T,L", [(32, 1, 4096), (16, 1, 37), (64, 1, 20000), (20, 8, 3000), (8, 64, 700)])
+@pytest.mark.parametrize("n_head,T,L", [(32, 1, 4096), (16, 1, 37), (64, 1, 20000), (20, 8, 3000), (8, 64, 700),
+                                         (32, 4, 33000)])
 def test_mla_matches_oracle(n_head, T, L):
     scale = 1.0 / np.sqrt(192)  # the engine's 1/sqrt(qk_nope)
     print(f"[case] mla h{n_head} T{T} L{L}", flush=True)
