@@ -77,10 +77,40 @@ __device__ __forceinline__ void lds_barrier() {
 // 16 bytes per lane from a buffer resource straight into LDS at
 // lds_base + 16 * lane (buffer_load_dwordx4 ... lds, base in M0).  Callers
 // wait for these loads (s_waitcnt vmcnt) before the barrier that publishes
-// the tile.
+// the tile.  `NT` sets the non-temporal bit (streamed data no one re-reads).
+template <bool NT = false>
 __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset, void* lds_base) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)lds_base, 16, voffset, 0,
-                                             0, 0);
+                                             0, NT ? 2 : 0);
+}
+
+// The same load issued from inline asm, so the compiler does not track it.
+// A tracked LDS DMA makes the compiler put s_waitcnt vmcnt(0) before any
+// later LDS read it cannot prove disjoint (the transposing ds_read_b64_tr_b16
+// reads always), which drains the whole prefetch ring — the next tiles'
+// loads included — in every loop iteration.  For loads issued inside a tile
+// loop: the kernel's own vmcnt waits and barriers order each tile's loads
+// before its reads, and every load is waited for before the loop ends, so
+// later LDS writes never race one.  Not for loads issued ahead of loads
+// the compiler waits for (queries): vmcnt counts in issue order, and the
+// compiler's count would not include these.  M0 is saved and restored.
+template <bool NT = false>
+__device__ __forceinline__ void lds_dma16_untracked(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset, void* lds_base) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(size_t)(__attribute__((address_space(3))) char*)lds_base);
+    uint32_t saved;
+    if constexpr (NT)
+        __asm__ volatile(
+            "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\t"
+            "buffer_load_dwordx4 %2, %3, 0 offen nt lds\n\ts_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "s"(m), "v"(voffset), "s"(rsrc));
+    else
+        __asm__ volatile(
+            "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\t"
+            "buffer_load_dwordx4 %2, %3, 0 offen lds\n\ts_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "s"(m), "v"(voffset), "s"(rsrc));
 }
 
 // Keys of sequence s: seq_len[s] clipped to kv_len (the bound every launch

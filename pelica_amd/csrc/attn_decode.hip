@@ -160,10 +160,14 @@ __device__ constexpr int k_swz_j(int j) {
 }
 
 // 16 bytes per lane from a buffer resource straight into LDS at lds + 16 *
-// lane, with the K/V stream's cache policy
-__device__ __forceinline__ void kv_dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset, char* lds) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, kKvAux);
+// lane, with the K/V stream's cache policy; `tracked` false: issued so the
+// compiler does not track it (loads inside the block loop, whose waits are
+// counted by hand; lds_dma16_untracked)
+__device__ __forceinline__ void kv_dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset, char* lds, bool tracked) {
+    if (tracked) lds_dma16<kKvAux == 2>(rsrc, voffset, lds);
+    else lds_dma16_untracked<kKvAux == 2>(rsrc, voffset, lds);
 }
+static_assert(kKvAux == 0 || kKvAux == 2, "K/V cache policy: default or nt");
 
 // s_waitcnt vmcnt(N), the other counters left alone (gfx9 encoding)
 template <int N>
@@ -468,17 +472,20 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     // Load j of a block fills LDS slots j*64 + lane of the wave's buffer
     // (buffer_load ... lds).  K of a block is requested before its V, so
     // QK^T can start while V is still arriving.
-    auto issue_k = [&](int i) {
+    // (block 0's loads are tracked by the compiler: the query loads below
+    // are waited for behind them; the loop's are not, see the loop)
+    auto issue_k = [&](int i, bool tracked) {
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) kv_dma16(rk, row_of(i, j) + 16 * (kcol0 ^ k_swz_j<HD>(j)), klds + 1024 * j);
+        for (int j = 0; j < VPL; ++j)
+            kv_dma16(rk, row_of(i, j) + 16 * (kcol0 ^ k_swz_j<HD>(j)), klds + 1024 * j, tracked);
     };
-    auto issue_v = [&](int i) {
+    auto issue_v = [&](int i, bool tracked) {
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) kv_dma16(rv, row_of(i, j) + vcol, vlds + 1024 * j);
+        for (int j = 0; j < VPL; ++j) kv_dma16(rv, row_of(i, j) + vcol, vlds + 1024 * j, tracked);
     };
     if (nb > 0) {
-        issue_k(0);
-        issue_v(0);
+        issue_k(0, true);
+        issue_v(0, true);
     }
 
     // ---- queries of this lane's rows: f16 parts (hi[, lo]) in base 2 ----
@@ -655,14 +662,16 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     // The vmcnt waits below are counted by hand from that order (VPL loads
     // per K or V block): the loop body, qk() and softmax_pv() must issue no
     // other vector-memory operation (no global or buffer load or store), or
-    // a wait would return before its block has landed.
+    // a wait would return before its block has landed.  The loop's loads
+    // are untracked by the compiler, which would otherwise wait for every
+    // outstanding load (K(i+1) too) before PV's transposing V reads.
     for (int i = 0; i < nb; ++i) {
         wait_vm<VPL>();  // K(i) landed
         if (i == 0) DTRACE(1);
         qk();
         wait_lgkm0();
         if (i + 1 < nb) {
-            issue_k(i + 1);
+            issue_k(i + 1, false);
             wait_vm<VPL>();  // V(i) landed
         } else {
             wait_vm<0>();
@@ -670,7 +679,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
         if (i < 2) DTRACE(2 + i);
         softmax_pv(blk(i));
         wait_lgkm0();
-        if (i + 1 < nb) issue_v(i + 1);
+        if (i + 1 < nb) issue_v(i + 1, false);
     }
     DTRACE(4);
     if (PK) {

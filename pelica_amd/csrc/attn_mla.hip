@@ -42,6 +42,25 @@ constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >>
 
 }  // namespace
 
+// Build-time instrumentation (off by default; -DPELICA_MTRACE): lane 0 of
+// wave 0 of each workgroup stores 100 MHz real-time stamps in
+// g_mtrace[workgroup * 32 + k]: 0 entry; for block i < 7, 1 + 4 i at the
+// loop top, 2 + 4 i once the block has landed (after the barrier), 3 + 4 i
+// after the score exchange, 4 + 4 i after PV; 29 loop end, 30 stores done,
+// 31 (XCC_ID << 32) | HW_ID (which CU ran it).  pelica_attn_debug_mtrace()
+// copies them out.
+#ifdef PELICA_MTRACE
+__device__ unsigned long long g_mtrace[1 << 15];
+#define MSTAMP(k)                                                                                          \
+    do {                                                                                                   \
+        if (tid == 0 && (k) < 32) g_mtrace[wg_lin * 32 + (k)] = __builtin_amdgcn_s_memrealtime();          \
+    } while (0)
+#else
+#define MSTAMP(k) \
+    do {          \
+    } while (0)
+#endif
+
 template <int RT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void mla_kernel(DecodeParams p) {
     constexpr int HD = kMlaHd, NW = 4, KB = 32;  // dims, waves, keys per block
@@ -61,6 +80,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
     const int rg = blockIdx.y, s = blockIdx.z, slot = blockIdx.x;
+#ifdef PELICA_MTRACE
+    const int wg_lin = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+    if (wg_lin >= 1024) return;
+    if (tid == 0)
+        g_mtrace[wg_lin * 32 + 31] = ((unsigned long long)__builtin_amdgcn_s_getreg(20 | (31 << 11)) << 32) |
+                                     (unsigned)__builtin_amdgcn_s_getreg(4 | (31 << 11));
+#endif
+    MSTAMP(0);
     const int len = seq_keys(p.seq_len, s, p.kv_len);
     if (len < p.T || len <= 0) return;
     const int n_active = min(p.n_slot, (len - 1) / p.split_keys + 1);
@@ -75,14 +102,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         (void*)(p.k + row0 * p.row_stride), (short)0, (int)((uint32_t)len * stride_b), kBufFlags);
     // block i -> LDS buffer i % NBUF; wave instruction j of wave w fills key
     // row 4 j + w (64 slots of 16 bytes); the lane loads the piece its slot holds
-    auto load_block = [&](int i) {
+    // (tracked: the prologue's loads, which the query loads are waited for
+    // around; untracked: the loop's, see lds_dma16_untracked)
+    auto load_block = [&](int i, bool tracked) {
         char* dst = lds + (i % NBUF) * BLK;
         const int kb = kbeg + KB * i;
 #pragma unroll
         for (int j = 0; j < KB / NW; ++j) {
             const int key = NW * j + wave;
             const int piece = lane ^ (key & 15);
-            lds_dma16(rs, (uint32_t)(kb + key) * stride_b + 16 * piece, dst + key * (HD * 2));
+            const uint32_t off = (uint32_t)(kb + key) * stride_b + 16 * piece;
+            if (tracked) lds_dma16(rs, off, dst + key * (HD * 2));
+            else lds_dma16_untracked(rs, off, dst + key * (HD * 2));
         }
     };
     // queries of this lane's rows, this wave's dims (requested before the
@@ -104,7 +135,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             qb2[rt][ds] = *reinterpret_cast<const float4v*>(qp + 32 * ds + 4);
         }
     }
-    for (int i = 0; i < NBUF - 1 && i < nblk; ++i) load_block(i);
+    for (int i = 0; i < NBUF - 1 && i < nblk; ++i) load_block(i, true);
     // f16 hi + lo parts, base 2
     half8 qf[NP][RT][DS];
 #pragma unroll
@@ -130,6 +161,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 
     for (int i = 0; i < nblk; ++i) {
+        if (i < 7) MSTAMP(1 + 4 * i);
         // block i is in LDS once at most the loads of the blocks issued after
         // it are outstanding (loads complete in order)
         const int later = min(nblk - 1 - i, NBUF - 2);
@@ -137,7 +169,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPB));
         else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         lds_barrier();  // ... for every wave; block i-1's readers are done
-        if (i + NBUF - 1 < nblk) load_block(i + NBUF - 1);  // into block i-1's buffer
+        if (i < 7) MSTAMP(2 + 4 * i);
+        if (i + NBUF - 1 < nblk) load_block(i + NBUF - 1, false);  // into block i-1's buffer
         const char* blk = lds + (i % NBUF) * BLK;
         const int kb = kbeg + KB * i;
 
@@ -181,6 +214,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     t4 += *reinterpret_cast<const float4v*>(part + (w * ROWS + 16 * rt + c16) * PS + 16 * kt + 4 * g);
                 sc[kt][rt] = t4;
             }
+        if (i < 7) MSTAMP(3 + 4 * i);
 
         // causal mask (only the blocks that reach past a row's position or
         // the split) and online softmax, identical in every wave; the running
@@ -250,7 +284,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
                 for (int rt = 0; rt < RT; ++rt) o[dt][rt] = mfma16(va, pf[pp][rt], o[dt][rt]);
         }
+        if (i < 7) MSTAMP(4 + 4 * i);
     }
+    MSTAMP(29);
 
     // this wave's dims of each row: the output, or the split's partial
 #pragma unroll
@@ -272,7 +308,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<float4v*>(op + 16 * dt) = o[dt][rt];
         }
     }
+#ifdef PELICA_MTRACE
+    __builtin_amdgcn_s_waitcnt(0);
+#endif
+    MSTAMP(30);
 }
+
+#ifdef PELICA_MTRACE
+extern "C" int pelica_attn_debug_mtrace(void* dst, size_t bytes) {
+    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_mtrace), bytes, 0, hipMemcpyDeviceToHost);
+}
+#endif
 
 hipError_t launch_mla(const DecodeParams& p, hipStream_t st) {
     if (p.rg_rows != 16) return hipErrorInvalidValue;

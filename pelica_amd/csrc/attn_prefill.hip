@@ -162,7 +162,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
     char* const vbuf = lds + (NRES ? NRES : 2) * TILE;  // V tiles
     // buffer of tile t: its own (resident) or t & 1 (streaming)
     auto tbuf = [](int t) { return NRES ? t : (t & 1); };
-    auto load_tile = [&](const __amdgpu_buffer_rsrc_t& rs, char* dst, int tile, bool is_v) {
+    // tracked: the prologue's loads; the chunk loop's are untracked (the
+    // compiler would wait for them before the PV's transposing V reads of
+    // the same chunk; the loop waits for them itself, at the next barrier)
+    auto load_tile = [&](const __amdgpu_buffer_rsrc_t& rs, char* dst, int tile, bool is_v, bool tracked) {
         const int kb = kb0 + 64 * tile;
 #pragma unroll
         for (int i = 0; i < WI; ++i) {
@@ -172,7 +175,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
             // (round rows before key_begin wrap to offsets past nrec: zeros)
             const uint32_t off = RING ? ((kb + key) % p.ring_cap) * stride_b + 16 * piece
                                       : (uint32_t)(kb + key - kbeg) * stride_b + 16 * piece;
-            lds_dma16(rs, off, dst + 1024 * (NW * i + wave));
+            if (tracked) lds_dma16(rs, off, dst + 1024 * (NW * i + wave));
+            else lds_dma16_untracked(rs, off, dst + 1024 * (NW * i + wave));
         }
     };
     // s_waitcnt vmcnt(0): the tile loads above have landed in LDS
@@ -288,12 +292,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
             *reinterpret_cast<u32x4*>(vzero + 16 * (tid + 64 * NW * i)) = u32x4{0, 0, 0, 0};
         if (NRES) {
             // (the launch guarantees n_tiles <= NRES)
-            for (int t = 0; t < n_tiles; ++t) load_tile(rk, kbuf + t * TILE, t, false);
-            for (int t = 0; t < n_tiles; ++t) load_tile(rv, vbuf + t * TILE, t, true);
+            for (int t = 0; t < n_tiles; ++t) load_tile(rk, kbuf + t * TILE, t, false, true);
+            for (int t = 0; t < n_tiles; ++t) load_tile(rv, vbuf + t * TILE, t, true, true);
         } else {
-            load_tile(rk, kbuf, 0, false);
-            if (n_tiles > 1) load_tile(rk, kbuf + TILE, 1, false);
-            load_tile(rv, vbuf, 0, true);
+            load_tile(rk, kbuf, 0, false, true);
+            if (n_tiles > 1) load_tile(rk, kbuf + TILE, 1, false, true);
+            load_tile(rv, vbuf, 0, true, true);
         }
         wait_tiles();
     }
@@ -323,8 +327,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
         // buffers' last readers finished at chunk 2t; first readers at 2t+3
         const int t = c >> 1;
         if (!NRES && (PAR & 1)) {
-            if (t + 2 < n_tiles) load_tile(rk, kbuf + (t & 1) * TILE, t + 2, false);
-            if (t + 1 < n_tiles) load_tile(rv, vbuf + ((t + 1) & 1) * TILE, t + 1, true);
+            if (t + 2 < n_tiles) load_tile(rk, kbuf + (t & 1) * TILE, t + 2, false, false);
+            if (t + 1 < n_tiles) load_tile(rv, vbuf + ((t + 1) & 1) * TILE, t + 1, true, false);
         }
 
         const int kb = kb0 + 32 * c;
