@@ -870,18 +870,21 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
 // per row (32 dims each).  ROW_WAVES: one wave per row (four rows per
 // workgroup, grid x = R / 4), for rows with few splits (<= 16): no LDS
 // stage, a quarter of the workgroups.
-template <int HD, bool ROW_WAVES>
+// dims per combine workgroup (DW): hd 128 in four slices of 32 (calls of
+// C2's size have only rows x kv heads = 32 rows: four times the workgroups
+// load the partials, 11.5 -> 11.3 us); hd 512 (MLA) in slices of 32 for
+// calls of <= 32 rows (16 heads x 32K latent rows: 18.9 -> 17.1 us), else
+// of 128 (a 64-token chunk has only 4 splits a row: slices of 32 leave most
+// threads idle, 102 -> 138 us)
+template <int HD, bool ROW_WAVES, int DW>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
     static_assert(!ROW_WAVES || HD <= 128, "one wave covers the row's dims");
-    // dims per workgroup: hd 128 in four slices of 32 (calls of C2's size
-    // have only rows x kv heads = 32 rows: four times the workgroups load
-    // the partials, 11.5 -> 11.3 us), hd 512 in four of 128
-    constexpr int DW = (HD == 128 && !ROW_WAVES) ? 32 : HD < 128 ? HD : 128;
+    static_assert(HD % DW == 0 && DW % 32 == 0 || DW == HD, "dims split into whole slices");
     constexpr int NQ = HD / DW;
     constexpr int D4 = DW / 4;
-    // phases: 16 (hd 64), 32 (hd 128), 8 (hd 512); one wave per row: 4, 2
+    // phases: 256 / (DW / 4) (16 at hd 64, 32 at DW 32); one wave per row: 4, 2
     constexpr int PH = (ROW_WAVES ? 64 : 256) / D4;
-    constexpr int J = DW < 128 && HD == 128 ? 4 : 8;  // splits per thread per pass
+    constexpr int J = DW < 128 && HD >= 128 ? 4 : 8;  // splits per thread per pass
     __shared__ float4v s_o[4][D4];
     __shared__ float2 s_ml[4][D4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1050,15 +1053,20 @@ hipError_t launch_combine(const DecodeParams& p, hipStream_t st) {
     ProfScope ps(kProfDecodeCombine, st);
     if (p.hd <= 128 && p.n_slot <= PELICA_COMBINE_ROW_WAVE_SLOTS) {
         const dim3 grid((p.R + 3) / 4, p.n_kv, p.n_seq);
-        if (p.hd == 64) hipLaunchKernelGGL((decode_combine_kernel<64, true>), grid, dim3(256), 0, st, p);
-        else hipLaunchKernelGGL((decode_combine_kernel<128, true>), grid, dim3(256), 0, st, p);
+        if (p.hd == 64) hipLaunchKernelGGL((decode_combine_kernel<64, true, 64>), grid, dim3(256), 0, st, p);
+        else hipLaunchKernelGGL((decode_combine_kernel<128, true, 128>), grid, dim3(256), 0, st, p);
         return hipGetLastError();
     }
-    const dim3 grid(p.R * (p.hd > 128 ? p.hd / 128 : p.hd == 128 ? 4 : 1), p.n_kv, p.n_seq);
+    auto grid = [&](int dw) { return dim3(p.R * (p.hd / dw), p.n_kv, p.n_seq); };
     switch (p.hd) {
-        case 64: hipLaunchKernelGGL((decode_combine_kernel<64, false>), grid, dim3(256), 0, st, p); break;
-        case 128: hipLaunchKernelGGL((decode_combine_kernel<128, false>), grid, dim3(256), 0, st, p); break;
-        case 512: hipLaunchKernelGGL((decode_combine_kernel<512, false>), grid, dim3(256), 0, st, p); break;
+        case 64: hipLaunchKernelGGL((decode_combine_kernel<64, false, 64>), grid(64), dim3(256), 0, st, p); break;
+        case 128: hipLaunchKernelGGL((decode_combine_kernel<128, false, 32>), grid(32), dim3(256), 0, st, p); break;
+        case 512:
+            if ((long long)p.R * p.n_seq <= 32)
+                hipLaunchKernelGGL((decode_combine_kernel<512, false, 32>), grid(32), dim3(256), 0, st, p);
+            else
+                hipLaunchKernelGGL((decode_combine_kernel<512, false, 128>), grid(128), dim3(256), 0, st, p);
+            break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -17,6 +17,8 @@
 // accumulates O^T[dims] += V^T[dims] P^T with V read by the transposing
 // ds_read_b64_tr_b16 (P split into hi + lo as the B operand).  HBM-bound:
 // per 32-key block 32 KB of latent against 128 MFMAs per wave.
+#include <type_traits>
+
 #include "attn_decode.hpp"
 #include "attn_prof.hpp"
 
@@ -78,7 +80,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     __shared__ __attribute__((aligned(16))) char lds[NBUF * BLK + NW * ROWS * PS * 4];
     float* const part = reinterpret_cast<float*>(lds + NBUF * BLK);  // [NW][ROWS][PS] partial scores
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+    // (the wave index scalar: addresses built from it stay in SGPRs)
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4,
+              c16 = lane & 15;
     const int rg = blockIdx.y, s = blockIdx.z, slot = blockIdx.x;
 #ifdef PELICA_MTRACE
     const int wg_lin = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
@@ -135,7 +139,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             qb2[rt][ds] = *reinterpret_cast<const float4v*>(qp + 32 * ds + 4);
         }
     }
-    for (int i = 0; i < NBUF - 1 && i < nblk; ++i) load_block(i, true);
+    if (nblk > 0) load_block(0, true);  // (a 2-block ring: the first fill is block 0)
     // f16 hi + lo parts, base 2
     half8 qf[NP][RT][DS];
 #pragma unroll
@@ -160,21 +164,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int dt = 0; dt < DT; ++dt) o[dt][rt] = float4v{0.f, 0.f, 0.f, 0.f};
     }
 
-    for (int i = 0; i < nblk; ++i) {
-        if (i < 7) MSTAMP(1 + 4 * i);
-        // block i is in LDS once at most the loads of the blocks issued after
-        // it are outstanding (loads complete in order)
-        const int later = min(nblk - 1 - i, NBUF - 2);
-        if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * LPB));
-        else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPB));
-        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-        lds_barrier();  // ... for every wave; block i-1's readers are done
-        if (i < 7) MSTAMP(2 + 4 * i);
-        if (i + NBUF - 1 < nblk) load_block(i + NBUF - 1, false);  // into block i-1's buffer
-        const char* blk = lds + (i % NBUF) * BLK;
-        const int kb = kbeg + KB * i;
-
-        // partial scores over this wave's dims: 2 key tiles x RT row tiles
+    // partial scores over this wave's dims: 2 key tiles x RT row tiles;
+    // element e of (kt, rt) is key 16 kt + 4 g + e of row 16 rt + c16
+    auto qk_part = [&](const char* blk, float4v (&pr)[2][RT]) {
         float4v acc[NP][2][RT];
 #pragma unroll
         for (int pp = 0; pp < NP; ++pp)
@@ -195,31 +187,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
                     for (int rt = 0; rt < RT; ++rt) acc[pp][kt][rt] = mfma16(ka[kt], qf[pp][rt][ds], acc[pp][kt][rt]);
         }
-        // element i of (kt, rt) is key 16 kt + 4 g + i of row 16 rt + c16
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) pr[kt][rt] = acc[0][kt][rt] + acc[1][kt][rt];
+    };
+    auto write_part = [&](float* pb, const float4v (&pr)[2][RT]) {
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt)
-                *reinterpret_cast<float4v*>(part + (wave * ROWS + 16 * rt + c16) * PS + 16 * kt + 4 * g) =
-                    acc[0][kt][rt] + acc[1][kt][rt];
-        lds_barrier();
-        float4v sc[2][RT];
+                *reinterpret_cast<float4v*>(pb + (wave * ROWS + 16 * rt + c16) * PS + 16 * kt + 4 * g) = pr[kt][rt];
+    };
+    auto read_sums = [&](const float* pb, float4v (&sc)[2][RT]) {
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) {
-                float4v t4 = {0.f, 0.f, 0.f, 0.f};
+                // (seeded with wave 0's partial: 0 + x is not x for x = -0)
+                float4v t4 = *reinterpret_cast<const float4v*>(pb + (16 * rt + c16) * PS + 16 * kt + 4 * g);
 #pragma unroll
-                for (int w = 0; w < NW; ++w)
-                    t4 += *reinterpret_cast<const float4v*>(part + (w * ROWS + 16 * rt + c16) * PS + 16 * kt + 4 * g);
+                for (int w = 1; w < NW; ++w)
+                    t4 += *reinterpret_cast<const float4v*>(pb + (w * ROWS + 16 * rt + c16) * PS + 16 * kt + 4 * g);
                 sc[kt][rt] = t4;
             }
-        if (i < 7) MSTAMP(3 + 4 * i);
-
-        // causal mask (only the blocks that reach past a row's position or
-        // the split) and online softmax, identical in every wave; the running
-        // max moves (O and l rescaled) only when a row's block max exceeds it
-        // by 2^8, so most blocks skip the rescale
+    };
+    // causal mask (only the blocks that reach past a row's position or the
+    // split) and online softmax, identical in every wave; the running max
+    // moves (O and l rescaled) only when a row's block max exceeds it by
+    // 2^8, so most blocks skip the rescale
+    auto softmax = [&](int i, float4v (&sc)[2][RT], half8 (&pf)[NPP][RT]) {
+        const int kb = kbeg + KB * i;
         if (kb + KB > kend || kb + KB - 1 > posr[0]) {
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt)
@@ -256,7 +254,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 }
             }
         }
-        half8 pf[NPP][RT];
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
             const float ms = m[rt] == -INFINITY ? 0.f : m[rt];
@@ -273,8 +270,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 }
             l[rt] += ls;
         }
-
-        // O^T[this wave's dims] += V^T P^T (keys in the B operand's order)
+    };
+    // O^T[this wave's dims] += V^T P^T (keys in the B operand's order)
+    auto pv = [&](const char* blk, const half8 (&pf)[NPP][RT]) {
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
             const int k0 = 4 * g + (c16 >> 2), d0 = 128 * wave + 16 * dt + 4 * (c16 & 3);
@@ -284,7 +282,41 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
                 for (int rt = 0; rt < RT; ++rt) o[dt][rt] = mfma16(va, pf[pp][rt], o[dt][rt]);
         }
+    };
+    // s_waitcnt: block j is in LDS once at most the loads of the `later`
+    // blocks issued after it are outstanding (loads complete in order)
+    auto wait_later = [&](int later) {
+        if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * LPB));
+        else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPB));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    };
+
+    // trip i on buffer PAR = i % 2, a compile-time constant (the loop is
+    // unrolled by two): every LDS address is then a loop-invariant lane
+    // offset plus an immediate
+    auto trip = [&](auto par, int i) {
+        constexpr int PAR = decltype(par)::value;
+        const char* const blk = lds + PAR * BLK;
+        if (i < 7) MSTAMP(1 + 4 * i);
+        wait_later(min(nblk - 1 - i, NBUF - 2));
+        lds_barrier();  // ... for every wave; block i-1's readers are done
+        if (i < 7) MSTAMP(2 + 4 * i);
+        if (i + 1 < nblk) load_block(i + 1, false);  // into block i-1's buffer
+        float4v pr[2][RT];
+        qk_part(blk, pr);
+        write_part(part, pr);
+        lds_barrier();
+        float4v sc[2][RT];
+        read_sums(part, sc);
+        if (i < 7) MSTAMP(3 + 4 * i);
+        half8 pf[NPP][RT];
+        softmax(i, sc, pf);
+        pv(blk, pf);
         if (i < 7) MSTAMP(4 + 4 * i);
+    };
+    for (int i = 0; i < nblk; i += 2) {
+        trip(std::integral_constant<int, 0>{}, i);
+        if (i + 1 < nblk) trip(std::integral_constant<int, 1>{}, i + 1);
     }
     MSTAMP(29);
 
