@@ -400,6 +400,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     constexpr int DT = HD / 16;   // 16-dim output tiles
     constexpr int VPL = HD / 8;   // 16-byte pieces per lane per block, each of K and V
     constexpr int ROWS = RT * 16;
+#ifdef PELICA_DEC_LATE_V
+    constexpr bool EARLY_V = false;
+#else
+    constexpr bool EARLY_V = HD == 64 && !SK;
+#endif
     // f16 parts of Q and P: packed (PK: hi in columns 0-7, lo in 8-15, one
     // MFMA), or NP separate passes
     constexpr int NP = PK ? 1 : kDecodeSplitParts;
@@ -554,12 +559,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds) kread[ds] = klds + c16 * (HD * 2) + 16 * ((g + 4 * ds) ^ k_swz<HD>(c16));
     float4v sc[4][RT];
-    auto qk = [&]() {
+    // after_reads: runs once the block's K operands are in registers (the
+    // K buffer is then free for the next block's loads)
+    auto qk = [&](auto&& after_reads) {
         half8 kc[4][DS];
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
             for (int ds = 0; ds < DS; ++ds) kc[kt][ds] = load16(kread[ds] + kt * 16 * (HD * 2));
+        after_reads();
         // independent accumulators per (part, key tile, row tile); the
         // k-steps run outermost so consecutive MFMAs do not depend on each other
         float4v acc[NP][4][RT];
@@ -589,7 +597,22 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
                 }
             }
     };
-    auto softmax_pv = [&](int kb) {
+    // EARLY_V (head dim 64: 32 more VGPRs fit): the block's V^T operands are
+    // read before the softmax and after_vreads() then runs (the V buffer is
+    // free for the next block's loads before the softmax, not after PV)
+    auto softmax_pv = [&](int kb, auto&& after_vreads) {
+        const _Float16* vb = reinterpret_cast<const _Float16*>(vlds);
+        half8 va_all[EARLY_V ? 2 : 1][DT];
+        if constexpr (EARLY_V) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    const int k0 = 32 * u + 4 * g + (c16 >> 2), d0 = 16 * dt + 4 * (c16 & 3);
+                    va_all[u][dt] = cat8(lds_read_tr(v_elem<HD>(vb, k0, d0)), lds_read_tr(v_elem<HD>(vb, k0 + 16, d0)));
+                }
+            after_vreads();
+        }
         // mask (blocks at a range boundary only): row r sees keys [lor, posr]
         if (kb < lo_hi || kb + 63 > pos_lo) {
 #pragma unroll
@@ -636,14 +659,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
             for (int dt = 0; dt < DT; ++dt) o[dt][rt] *= c;
         }
         // O^T += V^T P^T; the dim tiles are independent accumulators
-        const _Float16* vb = reinterpret_cast<const _Float16*>(vlds);
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             half8 va[DT];
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
                 const int k0 = 32 * u + 4 * g + (c16 >> 2), d0 = 16 * dt + 4 * (c16 & 3);
-                va[dt] = cat8(lds_read_tr(v_elem<HD>(vb, k0, d0)), lds_read_tr(v_elem<HD>(vb, k0 + 16, d0)));
+                va[dt] = EARLY_V ? va_all[EARLY_V ? u : 0][dt]
+                                 : cat8(lds_read_tr(v_elem<HD>(vb, k0, d0)), lds_read_tr(v_elem<HD>(vb, k0 + 16, d0)));
             }
 #pragma unroll
             for (int pp = 0; pp < NP; ++pp)
@@ -668,18 +691,21 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     for (int i = 0; i < nb; ++i) {
         wait_vm<VPL>();  // K(i) landed
         if (i == 0) DTRACE(1);
-        qk();
-        wait_lgkm0();
-        if (i + 1 < nb) {
-            issue_k(i + 1, false);
-            wait_vm<VPL>();  // V(i) landed
-        } else {
-            wait_vm<0>();
-        }
+        qk([&] {
+            wait_lgkm0();
+            if (i + 1 < nb) issue_k(i + 1, false);
+        });
+        if (i + 1 < nb) wait_vm<VPL>();  // V(i) landed
+        else wait_vm<0>();
         if (i < 2) DTRACE(2 + i);
-        softmax_pv(blk(i));
-        wait_lgkm0();
-        if (i + 1 < nb) issue_v(i + 1, false);
+        softmax_pv(blk(i), [&] {
+            wait_lgkm0();
+            if (i + 1 < nb) issue_v(i + 1, false);
+        });
+        if constexpr (!EARLY_V) {
+            wait_lgkm0();
+            if (i + 1 < nb) issue_v(i + 1, false);
+        }
     }
     DTRACE(4);
     if (PK) {
@@ -879,7 +905,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
 template <int HD, bool ROW_WAVES, int DW>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
     static_assert(!ROW_WAVES || HD <= 128, "one wave covers the row's dims");
-    static_assert(HD % DW == 0 && DW % 32 == 0 || DW == HD, "dims split into whole slices");
+    static_assert((HD % DW == 0 && DW % 32 == 0) || DW == HD, "dims split into whole slices");
     constexpr int NQ = HD / DW;
     constexpr int D4 = DW / 4;
     // phases: 256 / (DW / 4) (16 at hd 64, 32 at DW 32); one wave per row: 4, 2
