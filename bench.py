@@ -44,6 +44,9 @@ def parse():
     ap.add_argument("--only", default="", help="comma list of config names to time (default: all)")
     ap.add_argument("--profile", default="",
                     help="comma list of configs: just run each --steps times, eagerly, for rocprofv3 passes")
+    ap.add_argument("--ptrace", default="",
+                    help="comma list of prefill configs: summarise the prefill kernel's per-wave stamps "
+                         "(needs a library built with -DPELICA_PTRACE, loaded through PELICA_ATTN_LIB)")
     return ap.parse_args()
 
 
@@ -355,6 +358,52 @@ def profile_only(args):
         print(f"profiled {name} x{args.steps}", flush=True)
 
 
+def ptrace_summary(args):
+    """Shader clock and per-chunk cycles of the prefill kernel, from the
+    per-wave stamps of a -DPELICA_PTRACE build (pelica_attn_debug_ptrace):
+    [loop cycles (s_memtime), tile-wait cycles, barrier cycles, exact-path
+    chunks << 32 | chunks, then 100 MHz real-time stamps at entry, loop
+    start, loop end and exit] per wave, of the last of --steps calls."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from pelica_amd import attn
+    from pelica_amd import workloads as wl
+
+    lib = attn.load_library()
+    if not hasattr(lib, "pelica_attn_debug_ptrace"):
+        sys.exit("--ptrace needs a library built with -DPELICA_PTRACE (PELICA_ATTN_LIB)")
+    for name in args.ptrace.split(","):
+        cfg = wl.CONFIGS[name]
+        inp = wl.make_inputs(cfg, "cuda")
+        for _ in range(args.steps):
+            attn.prefill(inp.q, inp.k, inp.v, n_kv=cfg.n_kv, sinks=inp.sinks, window=cfg.window)
+        torch.cuda.synchronize()
+        buf = np.zeros(1 << 18, dtype=np.uint64)
+        rc = lib.pelica_attn_debug_ptrace(buf.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(buf.nbytes))
+        assert rc == 0, rc
+        raw = buf.reshape(-1, 8)
+        n_chunks = raw[:, 3] & np.uint64(0xFFFFFFFF)
+        keep = (raw[:, 7] > 0) & (n_chunks > 0)  # waves of the grid that ran the loop
+        w = raw[keep].astype(np.float64)
+        chunks = n_chunks[keep].astype(np.float64)
+        loop_us = (w[:, 6] - w[:, 5]) / 100.0
+        ghz = w[:, 0] / (loop_us * 1e3)
+        q = lambda a, p: float(np.percentile(a, p))
+        print(json.dumps({
+            "config": name, "waves": int(len(w)),
+            "shader_clock_GHz": {"median": round(q(ghz, 50), 3), "p10": round(q(ghz, 10), 3), "p90": round(q(ghz, 90), 3)},
+            "loop_cycles_per_chunk": round(q(w[:, 0] / chunks, 50), 1),
+            "tile_wait_frac": round(float(w[:, 1].sum() / w[:, 0].sum()), 4),
+            "barrier_frac": round(float(w[:, 2].sum() / w[:, 0].sum()), 4),
+            "entry_to_loop_us": round(q((w[:, 5] - w[:, 4]) / 100.0, 50), 2),
+            "loop_us": round(q(loop_us, 50), 2),
+            "loop_to_exit_us": round(q((w[:, 7] - w[:, 6]) / 100.0, 50), 2),
+        }), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -368,6 +417,8 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     if args.profile:
         return profile_only(args)
+    if args.ptrace:
+        return ptrace_summary(args)
     only = set(filter(None, args.only.split(",")))
 
     def want(c):
