@@ -363,7 +363,9 @@ def ptrace_summary(args):
     per-wave stamps of a -DPELICA_PTRACE build (pelica_attn_debug_ptrace):
     [loop cycles (s_memtime), tile-wait cycles, barrier cycles, exact-path
     chunks << 32 | chunks, then 100 MHz real-time stamps at entry, loop
-    start, loop end and exit] per wave, of the last of --steps calls."""
+    start, loop end and exit, after the prologue's loads are issued, after
+    they landed, after the workgroup barrier] per wave (16 words), of the
+    last of --steps calls."""
     import ctypes
 
     import numpy as np
@@ -384,7 +386,7 @@ def ptrace_summary(args):
         buf = np.zeros(1 << 18, dtype=np.uint64)
         rc = lib.pelica_attn_debug_ptrace(buf.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(buf.nbytes))
         assert rc == 0, rc
-        raw = buf.reshape(-1, 8)
+        raw = buf.reshape(-1, 16)
         n_chunks = raw[:, 3] & np.uint64(0xFFFFFFFF)
         keep = (raw[:, 7] > 0) & (n_chunks > 0)  # waves of the grid that ran the loop
         w = raw[keep].astype(np.float64)
@@ -399,6 +401,13 @@ def ptrace_summary(args):
             "tile_wait_frac": round(float(w[:, 1].sum() / w[:, 0].sum()), 4),
             "barrier_frac": round(float(w[:, 2].sum() / w[:, 0].sum()), 4),
             "entry_to_loop_us": round(q((w[:, 5] - w[:, 4]) / 100.0, 50), 2),
+            # waves that started in the second half of the kernel's span (later generations)
+            "entry_to_loop_us_late": round(q(((w[:, 5] - w[:, 4]) / 100.0)[w[:, 4] > np.median(w[:, 4])], 50), 2),
+            "span_us": round(float((w[:, 7].max() - w[:, 4].min()) / 100.0), 2),
+            "entry_to_issued_us": round(q((w[:, 8] - w[:, 4]) / 100.0, 50), 2),
+            "issued_to_landed_us": round(q((w[:, 9] - w[:, 8]) / 100.0, 50), 2),
+            "landed_to_barrier_us": round(q((w[:, 10] - w[:, 9]) / 100.0, 50), 2),
+            "barrier_to_loop_us": round(q((w[:, 5] - w[:, 10]) / 100.0, 50), 2),
             "loop_us": round(q(loop_us, 50), 2),
             "loop_to_exit_us": round(q((w[:, 7] - w[:, 6]) / 100.0, 50), 2),
         }), flush=True)

@@ -83,7 +83,9 @@ constexpr int kPrefillOcc = HD * RT >= 256 ? 1 : 2;
 // shader-clock cycles spent in the tile loop, waiting for tile loads and at
 // the per-chunk barrier, the number of exact-path chunks, and 100 MHz
 // real-time stamps at entry, loop start, loop end and exit (their ratio to
-// the cycle count gives the shader clock), stored in g_ptrace[wave * 8 + k];
+// the cycle count gives the shader clock), and in the prologue after the
+// query and tile loads are issued, after they landed and after the
+// workgroup barrier, stored in g_ptrace[wave * 16 + k];
 // pelica_attn_debug_ptrace() copies them out.
 #ifdef PELICA_PTRACE
 __device__ unsigned long long g_ptrace[1 << 18];
@@ -122,7 +124,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h2 = lane >> 5, c32 = lane & 31;
 #ifdef PELICA_PTRACE
     const unsigned long long rt_entry = rtime();
-    unsigned long long rt_loop0 = 0, rt_loop1 = 0;
+    unsigned long long rt_loop0 = 0, rt_loop1 = 0, rt_issued = 0, rt_landed = 0, rt_bar = 0;
 #endif
     const int len = seq_keys(p.seq_len, s, p.kv_len);
     if (len < p.T || len <= 0) return;
@@ -182,23 +184,50 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
     // s_waitcnt vmcnt(0): the tile loads above have landed in LDS
     auto wait_tiles = [] { __builtin_amdgcn_s_waitcnt(0x0F70); };
 
+    // The first tiles are requested before anything else, and nothing in
+    // the prologue after them waits for a load: the queries come through a
+    // buffer resource whose out-of-range offsets read as zeros (rows past
+    // the block need no select on loaded data) and the sink logits are
+    // loaded for every row.  (A select or a conditional load there makes
+    // the compiler wait for every load issued before it — with the tile
+    // requests behind it, a whole HBM round trip.)
+    // the (empty) PV of chunk -1 reads this zeroed tile: V tile 1's
+    // buffer (streaming) or the tile after the resident ones
+    char* const vzero = NRES ? lds + 2 * NRES * TILE : vbuf + TILE;
+    if (n_tiles > 0) {  // (uniform over the workgroup)
+#pragma unroll
+        for (int i = 0; i < TILE / (16 * 64 * NW); ++i)
+            *reinterpret_cast<u32x4*>(vzero + 16 * (tid + 64 * NW * i)) = u32x4{0, 0, 0, 0};
+        if (NRES) {
+            // (the launch guarantees n_tiles <= NRES)
+            for (int t = 0; t < n_tiles; ++t) load_tile(rk, kbuf + t * TILE, t, false, true);
+            for (int t = 0; t < n_tiles; ++t) load_tile(rv, vbuf + t * TILE, t, true, true);
+        } else {
+            load_tile(rk, kbuf, 0, false, true);
+            if (n_tiles > 1) load_tile(rk, kbuf + TILE, 1, false, true);
+            load_tile(rv, vbuf, 0, true, true);
+        }
+    }
+
     // this lane's query rows (column c32 of each 32-row tile): Q as the B
     // operand, position and window start
     half8 qb[RT][KS];
     int posr[RT], lor[RT];
     bool valid[RT];
+    const uint32_t qtok_b = (uint32_t)p.n_head * HD * 2;  // bytes of one token's query heads
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.q + ((size_t)s * p.T + t0) * p.n_head * HD), (short)0, (int)((uint32_t)(t1 - t0) * qtok_b),
+        kBufferFlags);
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
         const int r = (wave * RT + rt) * 32 + c32;
         const int t = t0 + r / p.hpk;
         valid[rt] = r < TB * p.hpk && t < t1;
         const int h = kvh * p.hpk + r % p.hpk;
-        const uint16_t* qp = p.q + ((size_t)(s * p.T + (valid[rt] ? t : t0)) * p.n_head + (valid[rt] ? h : 0)) * HD + 8 * h2;
+        const uint32_t qoff = valid[rt] ? (uint32_t)(t - t0) * qtok_b + (uint32_t)(h * HD + 8 * h2) * 2 : 0xFFFFFF00u;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            qb[rt][ks] = load16(qp + 16 * ks);
-            if (!valid[rt]) qb[rt][ks] = half8{0, 0, 0, 0, 0, 0, 0, 0};
-        }
+        for (int ks = 0; ks < KS; ++ks)
+            qb[rt][ks] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + 32 * ks, 0, 0));
         posr[rt] = valid[rt] ? len - p.T + t : -1;
         lor[rt] = (p.window > 0 && posr[rt] + 1 > p.window) ? posr[rt] + 1 - p.window : 0;
     }
@@ -210,10 +239,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
     for (int rt = 0; rt < RT; ++rt) {
         m[rt] = valid[rt] ? -INFINITY : 0.f;  // rows past the block: all masked, fast path
         l[rt] = 0.f;
-        if (!ROUND && p.sinks && valid[rt]) {
+        if (!ROUND && p.sinks) {  // (every row's index is a head of this kv head)
             const int r = (wave * RT + rt) * 32 + c32;
-            m[rt] = p.sinks[kvh * p.hpk + r % p.hpk] * kLog2e;
-            l[rt] = h2 == 0 ? 1.f : 0.f;
+            const float sk = p.sinks[kvh * p.hpk + r % p.hpk] * kLog2e;
+            m[rt] = valid[rt] ? sk : m[rt];
+            l[rt] = valid[rt] && h2 == 0 ? 1.f : 0.f;
         }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) o[dt][rt] = float16v{};
@@ -282,26 +312,20 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
     // maximum far above m) the wave takes the exact path: chunk max, rescale
     // O and l, recompute P.
     constexpr float kSumLimit = 16384.f;
-    // the (empty) PV of chunk -1 reads this zeroed tile: V tile 1's
-    // buffer (streaming) or the tile after the resident ones
-    char* const vzero = NRES ? lds + 2 * NRES * TILE : vbuf + TILE;
     if (n_tiles > 0) {  // (uniform over the workgroup)
     {
-#pragma unroll
-        for (int i = 0; i < TILE / (16 * 64 * NW); ++i)
-            *reinterpret_cast<u32x4*>(vzero + 16 * (tid + 64 * NW * i)) = u32x4{0, 0, 0, 0};
-        if (NRES) {
-            // (the launch guarantees n_tiles <= NRES)
-            for (int t = 0; t < n_tiles; ++t) load_tile(rk, kbuf + t * TILE, t, false, true);
-            for (int t = 0; t < n_tiles; ++t) load_tile(rv, vbuf + t * TILE, t, true, true);
-        } else {
-            load_tile(rk, kbuf, 0, false, true);
-            if (n_tiles > 1) load_tile(rk, kbuf + TILE, 1, false, true);
-            load_tile(rv, vbuf, 0, true, true);
-        }
+#ifdef PELICA_PTRACE
+        rt_issued = rtime();
+#endif
         wait_tiles();
+#ifdef PELICA_PTRACE
+        rt_landed = rtime();
+#endif
     }
     __syncthreads();
+#ifdef PELICA_PTRACE
+    rt_bar = rtime();
+#endif
 
 #ifdef PELICA_PTRACE
     unsigned t_wait = 0, t_bar = 0, n_exact = 0;
@@ -551,10 +575,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
     rt_loop1 = rtime();
     if (lane == 0) {
         const int wid = blockIdx.x * NW + wave;
-        g_ptrace[wid * 8 + 0] = cyc() - t_start;
-        g_ptrace[wid * 8 + 1] = t_wait;
-        g_ptrace[wid * 8 + 2] = t_bar;
-        g_ptrace[wid * 8 + 3] = (unsigned long long)n_exact << 32 | (unsigned)n_chunks;
+        g_ptrace[wid * 16 + 0] = cyc() - t_start;
+        g_ptrace[wid * 16 + 1] = t_wait;
+        g_ptrace[wid * 16 + 2] = t_bar;
+        g_ptrace[wid * 16 + 3] = (unsigned long long)n_exact << 32 | (unsigned)n_chunks;
     }
 #endif
     }
@@ -640,10 +664,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
     // (stores issued; the wave ends when they are done)
     if (lane == 0) {
         const int wid = blockIdx.x * NW + wave;
-        g_ptrace[wid * 8 + 4] = rt_entry;
-        g_ptrace[wid * 8 + 5] = rt_loop0;
-        g_ptrace[wid * 8 + 6] = rt_loop1;
-        g_ptrace[wid * 8 + 7] = rtime();
+        g_ptrace[wid * 16 + 4] = rt_entry;
+        g_ptrace[wid * 16 + 5] = rt_loop0;
+        g_ptrace[wid * 16 + 6] = rt_loop1;
+        g_ptrace[wid * 16 + 7] = rtime();
+        g_ptrace[wid * 16 + 8] = rt_issued;
+        g_ptrace[wid * 16 + 9] = rt_landed;
+        g_ptrace[wid * 16 + 10] = rt_bar;
     }
 #endif
 }
