@@ -1,13 +1,13 @@
-// Issue cost of the vector instructions of the prefill softmax, two waves per
-// SIMD (256 workgroups of 8 waves): s_memtime units per wave instruction per
-// SIMD, 8 independent chains, 256 x 64 instructions per wave.  exp_f32 vs
-// exp_f16 (plain and SDWA halves), fma_f32, fma_mix (f32 in, f16 half out),
-// cvt_pk_f16_f32.
+// Issue cost of the vector instructions of the prefill softmax for one wave
+// alone on its SIMD (256 workgroups of 4 waves): shader cycles (s_memtime)
+// per wave instruction, 8 independent chains, 256 x 64 instructions per
+// wave.  exp_f32 vs exp_f16 (plain and SDWA halves), fma_f32, fma_mix (f32
+// in, f16 half out), cvt_pk_f16_f32.
 #include <hip/hip_runtime.h>
 #include <cstdio>
 #define REP8(x) x x x x x x x x
 template <int K>
-__global__ __launch_bounds__(512) void bench(float* out, unsigned long long* cyc, float a) {
+__global__ __launch_bounds__(256) void bench(float* out, unsigned long long* cyc, float a) {
     float r0 = a + threadIdx.x, r1 = r0 + 1, r2 = r0 + 2, r3 = r0 + 3, r4 = r0 + 4, r5 = r0 + 5, r6 = r0 + 6, r7 = r0 + 7;
     unsigned long long t0 = __builtin_amdgcn_s_memtime();
     for (int it = 0; it < 256; ++it) {
@@ -19,18 +19,18 @@ __global__ __launch_bounds__(512) void bench(float* out, unsigned long long* cyc
         if (K == 5) asm volatile(REP8("v_cvt_pk_f16_f32 %0, %1, %2\n v_cvt_pk_f16_f32 %1, %2, %3\n v_cvt_pk_f16_f32 %2, %3, %4\n v_cvt_pk_f16_f32 %3, %4, %5\n v_cvt_pk_f16_f32 %4, %5, %6\n v_cvt_pk_f16_f32 %5, %6, %7\n v_cvt_pk_f16_f32 %6, %7, %0\n v_cvt_pk_f16_f32 %7, %0, %1\n") : "+v"(r0), "+v"(r1), "+v"(r2), "+v"(r3), "+v"(r4), "+v"(r5), "+v"(r6), "+v"(r7));
     }
     unsigned long long t1 = __builtin_amdgcn_s_memtime();
-    out[blockIdx.x * 512 + threadIdx.x] = r0 + r1 + r2 + r3 + r4 + r5 + r6 + r7;
+    out[blockIdx.x * 256 + threadIdx.x] = r0 + r1 + r2 + r3 + r4 + r5 + r6 + r7;
     if (threadIdx.x == 0) cyc[blockIdx.x] = t1 - t0;
 }
 template <int K> void run(const char* name, float* out, unsigned long long* cyc) {
-    hipLaunchKernelGGL(bench<K>, dim3(256), dim3(512), 0, 0, out, cyc, 0.f);
-    hipLaunchKernelGGL(bench<K>, dim3(256), dim3(512), 0, 0, out, cyc, 0.f);
+    hipLaunchKernelGGL(bench<K>, dim3(256), dim3(256), 0, 0, out, cyc, 0.f);
+    hipLaunchKernelGGL(bench<K>, dim3(256), dim3(256), 0, 0, out, cyc, 0.f);
     (void)hipDeviceSynchronize();
     unsigned long long h[256];
     (void)hipMemcpy(h, cyc, sizeof h, hipMemcpyDeviceToHost);
     unsigned long long s = 0; for (int i = 0; i < 256; ++i) s += h[i];
-    // per SIMD: 2 waves x 256 x 64 instructions
-    printf("%-16s %.2f memtime cycles per instruction per SIMD (2 waves)\n", name, (double)s / 256 / (2 * 256 * 64));
+    // wave 0 of each workgroup: 256 x 64 instructions
+    printf("%-16s %.2f shader cycles per wave instruction (one wave per SIMD)\n", name, (double)s / 256 / (256 * 64));
 }
 int main() {
     float* out; unsigned long long* cyc;
