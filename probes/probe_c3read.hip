@@ -26,10 +26,14 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t off, vo
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, off, 0, 0, 2);
 }
 __device__ __forceinline__ void wait_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+__device__ __forceinline__ char* kb_lds(char (*lds)[16384], int wave) { return lds[wave]; }
+__device__ __forceinline__ char* kb_lds_k(char* w, int j) { return w + 1024 * j; }
 
 // MODE 0: both blocks of a wave requested at once (into the same LDS buffer)
 // MODE 1: the second block requested after the first has landed (the kernel's dependency)
 // MODE 2: whole 1 KB rows, one key per load: a workgroup takes 128 keys of all 8 heads
+// MODE 3: one kv head per XCD: workgroup i (on XCD i % 8) reads head i % 8 of keys
+//         [1024 (i / 8), +1024), its 8 waves two 64-key blocks each (8 keys x 128 B per load)
 template <int MODE>
 __global__ __launch_bounds__(512) void c3read(const char* k, const char* v, unsigned* sink) {
     __shared__ __attribute__((aligned(16))) char lds[8][16384];
@@ -38,7 +42,24 @@ __global__ __launch_bounds__(512) void c3read(const char* k, const char* v, unsi
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)v, 0, kRows * kRowBytes, 0x00020000);
     char* kb = lds[wave];
     char* vb = kb + 8192;
-    if (MODE == 2) {
+    if (MODE == 3) {
+        const int head = blockIdx.x & 7, key0 = (blockIdx.x >> 3) * 1024;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int kb = key0 + 64 * (wave + 8 * i);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t off = (uint32_t)(kb + 8 * j + lane / 8) * kRowBytes + head * 128 + 16 * (lane % 8);
+                dma16(rk, off, kb_lds_k(kb_lds(lds, wave), j));
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t off = (uint32_t)(kb + 8 * j + lane / 8) * kRowBytes + head * 128 + 16 * (lane % 8);
+                dma16(rv, off, kb_lds(lds, wave) + 8192 + 1024 * j);
+            }
+            wait_all();
+        }
+    } else if (MODE == 2) {
         const int key0 = blockIdx.x * 128 + wave * 16;
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
@@ -83,10 +104,10 @@ int main() {
     CK(hipMalloc(&sink, 64));
     hipStream_t st;
     CK(hipStreamCreate(&st));
-    const char* names[3] = {"split pattern, both blocks requested at once", "split pattern, second block after the first landed",
-                            "whole 1 KB rows, one key per load"};
+    const char* names[4] = {"split pattern, both blocks requested at once", "split pattern, second block after the first landed",
+                            "whole 1 KB rows, one key per load", "one kv head per XCD, second block after the first"};
     for (int rep = 0; rep < 2; ++rep)
-        for (int mode = 0; mode < 3; ++mode) {
+        for (int mode = 0; mode < 4; ++mode) {
             hipGraph_t g;
             hipGraphExec_t ge;
             CK(hipStreamBeginCapture(st, hipStreamCaptureModeGlobal));
@@ -96,6 +117,7 @@ int main() {
                 if (mode == 0) hipLaunchKernelGGL(c3read<0>, dim3(256), dim3(512), 0, st, kk, vv, sink);
                 if (mode == 1) hipLaunchKernelGGL(c3read<1>, dim3(256), dim3(512), 0, st, kk, vv, sink);
                 if (mode == 2) hipLaunchKernelGGL(c3read<2>, dim3(256), dim3(512), 0, st, kk, vv, sink);
+                if (mode == 3) hipLaunchKernelGGL(c3read<3>, dim3(256), dim3(512), 0, st, kk, vv, sink);
             }
             CK(hipStreamEndCapture(st, &g));
             CK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
