@@ -44,6 +44,9 @@ def parse():
     ap.add_argument("--only", default="", help="comma list of config names to time (default: all)")
     ap.add_argument("--profile", default="",
                     help="comma list of configs: just run each --steps times, eagerly, for rocprofv3 passes")
+    ap.add_argument("--dtrace", default="",
+                    help="comma list of decode configs: summarise the split kernel's per-wave stamps "
+                         "(needs a library built with -DPELICA_DTRACE, loaded through PELICA_ATTN_LIB)")
     ap.add_argument("--ptrace", default="",
                     help="comma list of prefill configs: summarise the prefill kernel's per-wave stamps "
                          "(needs a library built with -DPELICA_PTRACE, loaded through PELICA_ATTN_LIB)")
@@ -413,6 +416,59 @@ def ptrace_summary(args):
         }), flush=True)
 
 
+def dtrace_summary(args):
+    """Timeline of the decode split kernel from the per-wave stamps of a
+    -DPELICA_DTRACE build (pelica_attn_debug_trace): 100 MHz real-time
+    stamps at wave start, first K block landed, V blocks 0 and 1 landed,
+    loop end, merge hand-off (waves that do not merge) and end, plus the
+    wave's XCC/hardware id; of the last of --steps calls, in us from the
+    earliest wave start."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from pelica_amd import attn
+    from pelica_amd import workloads as wl
+
+    lib = attn.load_library()
+    if not hasattr(lib, "pelica_attn_debug_trace"):
+        sys.exit("--dtrace needs a library built with -DPELICA_DTRACE (PELICA_ATTN_LIB)")
+    for name in args.dtrace.split(","):
+        cfg = wl.CONFIGS[name]
+        inp = wl.make_inputs(cfg, "cuda")
+        kw = dict(n_kv=cfg.n_kv, kv_len=inp.kv_len, sinks=inp.sinks, window=cfg.window)
+        if inp.ragged:
+            kw.update(seq_kv_len=inp.seq_len, seq_kv_offset=inp.seq_off)
+        for _ in range(args.steps):
+            attn.decode(inp.q, inp.k, inp.v, **kw)
+        torch.cuda.synchronize()
+        buf = np.zeros(1 << 16, dtype=np.uint64)
+        rc = lib.pelica_attn_debug_trace(buf.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(buf.nbytes))
+        assert rc == 0, rc
+        w = buf.reshape(-1, 8)
+        w = w[w[:, 0] > 0]
+        # this call's waves: stamps within 1 ms of the latest start (the
+        # buffer keeps earlier calls' entries past this grid's waves)
+        w = w[w[:, 0] + 100000 > w[:, 0].max()]
+        t0 = float(w[:, 0].min())
+        rel = lambda col: (w[:, col].astype(np.float64) - t0) / 100.0
+        q = lambda a: [round(float(np.percentile(a, p)), 2) for p in (10, 50, 90)]
+        ok = lambda col: w[:, col] > 0
+        out = {"config": name, "waves": int(len(w)), "pct": "p10/p50/p90 us from the first wave's start"}
+        last = w[:, 6] > 0  # waves that wrote a result (the merging wave of each head)
+        for col, key in ((0, "start"), (1, "first_k_landed"), (2, "v0_landed"), (3, "v1_landed"), (4, "loop_end"),
+                         (6, "end")):
+            m = ok(col)
+            if m.any():
+                out[key] = q(rel(col)[m])
+        if last.any():
+            out["merging_wave_loop_to_merged_us"] = q(((w[:, 5].astype(np.float64) - w[:, 4]) / 100.0)[last & ok(5)])
+            out["merging_wave_merged_to_end_us"] = q(((w[:, 6].astype(np.float64) - w[:, 5]) / 100.0)[last & ok(5)])
+        out["last_end_us"] = round(float(rel(6)[ok(6)].max()), 2) if ok(6).any() else None
+        print(json.dumps(out), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -428,6 +484,8 @@ def main():
         return profile_only(args)
     if args.ptrace:
         return ptrace_summary(args)
+    if args.dtrace:
+        return dtrace_summary(args)
     only = set(filter(None, args.only.split(",")))
 
     def want(c):

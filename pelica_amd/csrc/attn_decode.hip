@@ -128,7 +128,8 @@ __device__ __forceinline__ void store_part(float* slot, int d, float m2, float l
 // Build-time instrumentation (off by default; -DPELICA_DTRACE): lane 0 of
 // every split-kernel wave stores s_memrealtime stamps (100 MHz) at start,
 // first K block landed, V blocks 0 and 1 landed, loop end, merge hand-off
-// and end, plus its XCC/hardware id, into g_dtrace[wave * 8 + k] (the
+// (the merging wave: merge done) and end, plus its XCC/hardware id, into
+// g_dtrace[wave * 8 + k] (the
 // first 8192 waves of the grid);
 // pelica_attn_debug_trace() copies the array out after a call.
 #ifdef PELICA_DTRACE
@@ -774,6 +775,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
         }
     }
 
+    if (W > 1) DTRACE(5);  // (the merging wave: merge done)
     // this lane's result: row 16 rt + c16 (PK: c16 < 8), dims 16 dt + 4 g
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
