@@ -161,8 +161,13 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl, bool allow_fuse = true)
     // Ragged batches without window or ring go stream-K: a fixed grid shares
     // the batch's blocks evenly, whatever the spread of the lengths (with
     // one split grid the longest sequences' workgroups set the time)
+    // (the kernel counts list positions in 32 bits: at most 2^31 - 1, with
+    // every sequence at kv_len and the start-up charge)
+    const int sk_restart = tn.sk_restart >= 0 ? tn.sk_restart : 8;
+    const long long sk_positions =
+        groups * ((long long)ceil_div(d->kv_len, 64) + sk_restart);
     const bool sk = d->seq_kv_len && d->window == 0 && d->ring_cap == 0 && !(d->hd == 64 && rt == 4) &&
-                    tn.streamk && tn.split_blocks == 0;
+                    tn.streamk && tn.split_blocks == 0 && sk_positions < 0x7fffffffLL;
     const bool big = !sk && pelica::decode_can_use_8_waves(d->hd, rt) && blocks >= 2048 && d->n_kv % 4 == 0;
     const int wg_heads = big ? 4 : 1;
     // 64-key blocks per wave: enough waves for every SIMD, each streaming
@@ -215,7 +220,7 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl, bool allow_fuse = true)
         // (a piece's start-up is charged as sk_restart blocks: ~15 us of
         // pipeline refill against ~1.4 us per block of a workgroup's
         // stream; 8 measured best, 6-14 within 1.5 %)
-        const int restart = tn.sk_restart >= 0 ? tn.sk_restart : 8;
+        const int restart = sk_restart;
         const int maxblk = ceil_div(d->kv_len, 64);
         const long long bmax = (long long)d->n_seq * d->n_kv * n_rg * (maxblk + restart);
         int minb = (int)std::min<long long>(64, std::max<long long>(4, bmax / (2LL * pl->sk_grid)));

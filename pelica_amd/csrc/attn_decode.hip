@@ -196,50 +196,79 @@ __device__ __forceinline__ float ror8(float x) {
 // range crosses a segment start gets correspondingly fewer blocks.  Each
 // piece of a segment is one split (slot = its index among the segment's
 // pieces).
+// List positions are 32-bit: the planner takes stream-K only for lists under
+// 2^31 positions (64-bit divisions and their register pressure cost the
+// kernel's prologue microseconds before its first load).
 struct SkLayout {
-    long long total;  // positions in the list
+    int total;          // positions in the list
     int g_eff, q, rem;  // workgroups used; range of w: q blocks (+1 if w < rem)
-    __device__ long long start(int w) const { return (long long)w * q + min(w, rem); }
+    __device__ int start(int w) const { return w * q + min(w, rem); }
     // the workgroup whose range holds block x
-    __device__ int owner(long long x) const {
-        const long long big = (long long)rem * (q + 1);
-        return x < big ? (int)(x / (q + 1)) : rem + (int)((x - big) / q);
+    __device__ int owner(int x) const {
+        const int big = rem * (q + 1);
+        return x < big ? x / (q + 1) : rem + (x - big) / q;
     }
 };
 
-// a wave-uniform 64-bit value as a scalar
-__device__ __forceinline__ long long uniform64(long long x) {
-    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)x);
-    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)((unsigned long long)x >> 32));
-    return (long long)((unsigned long long)hi << 32 | lo);
-}
+__device__ __forceinline__ int uniform32(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
-// blocks of sequence s in the stream-K list (0 for a skipped sequence)
-__device__ __forceinline__ int sk_blocks(const DecodeParams& p, int s) {
-    const int len = seq_keys(p.seq_len, s, p.kv_len);
+// blocks of a sequence of len keys in the stream-K list (0 for a skipped sequence)
+__device__ __forceinline__ int sk_blocks_of(const DecodeParams& p, int len) {
     return (len < p.T || len <= 0) ? 0 : (len + 63) / 64;
 }
-// list positions of one segment of sequence s (start-up + blocks, or 0)
-__device__ __forceinline__ int sk_span(const DecodeParams& p, int s) {
-    const int nb = sk_blocks(p, s);
+// list positions of one segment of a sequence of len keys (start-up + blocks, or 0)
+__device__ __forceinline__ int sk_span_of(const DecodeParams& p, int len) {
+    const int nb = sk_blocks_of(p, len);
     return nb ? nb + p.sk_restart : 0;
 }
 
-// the layout, computed by every lane of the calling wave (uniform result)
-__device__ SkLayout sk_layout(const DecodeParams& p, int gy) {
+// The batch's sequence tables as the stream-K driver reads them: for up to
+// 64 sequences lane i holds sequence i's key count and first cache row,
+// loaded once (one memory round trip for both) and read with readlane
+// afterwards; larger batches read the tables from memory each time.
+struct SeqTables {
+    bool cached;
+    int len;         // this lane's sequence's keys (cached)
+    long long off;   // its first cache row (cached)
+    __device__ int keys(const DecodeParams& p, int s) const {  // s uniform
+        return cached ? __builtin_amdgcn_readlane(len, s) : seq_keys(p.seq_len, s, p.kv_len);
+    }
+    __device__ int keys_lane(const DecodeParams& p, int s) const {  // s = base + lane
+        return cached ? len : seq_keys(p.seq_len, s, p.kv_len);
+    }
+    __device__ long long row0(const DecodeParams& p, int s) const {  // s uniform
+        if (!cached) return p.seq_off ? p.seq_off[s] : (long long)s * p.kv_len;
+        const unsigned lo = __builtin_amdgcn_readlane((unsigned)off, s);
+        const unsigned hi = __builtin_amdgcn_readlane((unsigned)((unsigned long long)off >> 32), s);
+        return (long long)((unsigned long long)hi << 32 | lo);
+    }
+};
+
+__device__ __forceinline__ SeqTables seq_tables(const DecodeParams& p) {
     const int lane = threadIdx.x & 63;
-    long long tot = 0;
+    SeqTables t{p.n_seq <= 64, 0, 0};
+    if (t.cached && lane < p.n_seq) {
+        t.len = seq_keys(p.seq_len, lane, p.kv_len);
+        t.off = p.seq_off ? p.seq_off[lane] : (long long)lane * p.kv_len;
+    }
+    return t;
+}
+
+// the layout, computed by every lane of the calling wave (uniform result)
+__device__ SkLayout sk_layout(const DecodeParams& p, int gy, const SeqTables& tb) {
+    const int lane = threadIdx.x & 63;
+    int tot = 0;
     for (int base = 0; base < p.n_seq; base += 64) {
-        long long x = base + lane < p.n_seq ? sk_span(p, base + lane) : 0;
+        int x = base + lane < p.n_seq ? sk_span_of(p, tb.keys_lane(p, base + lane)) : 0;
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
         tot += x;
     }
     SkLayout L;
-    L.total = uniform64(tot * gy);
-    L.g_eff = __builtin_amdgcn_readfirstlane((int)max(1LL, min((long long)p.sk_grid, L.total / p.sk_minb)));
-    L.q = __builtin_amdgcn_readfirstlane((int)(L.total / L.g_eff));
-    L.rem = __builtin_amdgcn_readfirstlane((int)(L.total % L.g_eff));
+    L.total = uniform32(tot * gy);
+    L.g_eff = uniform32(max(1, min(p.sk_grid, L.total / p.sk_minb)));
+    L.q = uniform32(L.total / L.g_eff);
+    L.rem = uniform32(L.total % L.g_eff);
     return L;
 }
 
@@ -431,10 +460,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     // One split: keys [kbeg, kend) of sequence s, row group and kv heads of
     // by, written to slot `slot` (single: the only split of its rows, which
     // then writes the output itself).  Uniform over the workgroup.
-    auto split = [&](const int s, const int by, const int len, const int kbeg, const int kend, const int slot,
-                     const bool single) {
+    auto split = [&](const int s, const int by, const int len, const int64_t row0, const int kbeg, const int kend,
+                     const int slot, const bool single) {
     const int kvh = (by % hgroups) * H + hl, rg = by / hgroups;
-    const int64_t row0 = p.seq_off ? p.seq_off[s] : (int64_t)s * (p.ring_cap ? p.ring_cap : p.kv_len);
     const int lo_min = key_range(len, p.T, 0, p.window).lo;
     const int rbase = rg * ROWS;
 
@@ -828,59 +856,61 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
         const int n_active = min(p.n_slot, (len - 1) / p.split_keys - split0 + 1);
         if (slot >= n_active) return;
         const int kbeg = (split0 + slot) * p.split_keys;
-        split(s, by, len, kbeg, min(kbeg + p.split_keys, len), slot, n_active == 1);
+        const int64_t row0 = p.seq_off ? p.seq_off[s] : (int64_t)s * (p.ring_cap ? p.ring_cap : p.kv_len);
+        split(s, by, len, row0, kbeg, min(kbeg + p.split_keys, len), slot, n_active == 1);
         if (p.fuse && n_active > 1 && !p.split_only) fused_merge<HD, H>(p, s, by, len, slot, n_active, &s_last);
         return;
     }
     // stream-K: this workgroup's range of the block list, piece by piece
     const int gy = hgroups * p.n_rg;
-    const SkLayout L = sk_layout(p, gy);
+    const SeqTables tb = seq_tables(p);
+    const SkLayout L = sk_layout(p, gy, tb);
     const int w = blockIdx.x;
     if (w >= L.g_eff || L.total == 0) return;
-    long long cur = L.start(w);
-    const long long end = L.start(w + 1);
+    int cur = L.start(w);
+    const int end = L.start(w + 1);
     if (cur >= end) return;
     // the sequence holding position cur (< total, so some lane of the scan
     // finds it), and the positions before it
     int s = 0;
-    long long pre = 0;  // positions before sequence s
+    int pre = 0;  // positions before sequence s
     for (int base = 0; base < p.n_seq; base += 64) {
-        const long long x = base + lane < p.n_seq ? (long long)sk_span(p, base + lane) * gy : 0;
-        long long incl = x;
+        const int x = base + lane < p.n_seq ? sk_span_of(p, tb.keys_lane(p, base + lane)) * gy : 0;
+        int incl = x;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
-            const long long y = __shfl_up(incl, off, 64);
+            const int y = __shfl_up(incl, off, 64);
             if (lane >= off) incl += y;
         }
         const unsigned long long hit = __builtin_amdgcn_ballot_w64(pre + incl > cur);
         if (hit) {
             const int j = __builtin_ctzll(hit);
             s = base + j;
-            pre = uniform64(pre + __shfl(incl - x, j, 64));
+            pre = uniform32(pre + __shfl(incl - x, j, 64));
             break;
         }
-        pre = uniform64(pre + __shfl(incl, 63, 64));
+        pre = uniform32(pre + __shfl(incl, 63, 64));
     }
     while (cur < end && s < p.n_seq) {
-        const int nb = __builtin_amdgcn_readfirstlane(sk_blocks(p, s));
+        const int len = uniform32(tb.keys(p, s));
+        const int nb = sk_blocks_of(p, len);
         const int span = nb ? nb + p.sk_restart : 0;
-        if (nb == 0 || cur >= pre + (long long)span * gy) {  // past this sequence
-            pre += (long long)span * gy;
+        if (nb == 0 || cur >= pre + span * gy) {  // past this sequence
+            pre += span * gy;
             ++s;
             continue;
         }
-        const int len = __builtin_amdgcn_readfirstlane(seq_keys(p.seq_len, s, p.kv_len));
-        const int by = (int)((cur - pre) / span);
-        const long long seg = pre + (long long)by * span + p.sk_restart;  // the segment's first block
+        const int by = (cur - pre) / span;
+        const int seg = pre + by * span + p.sk_restart;  // the segment's first block
         if (cur < seg) {  // (in the start-up positions)
             cur = seg;
             if (cur >= end) break;
         }
-        const long long pend = min(end, seg + nb);
+        const int pend = min(end, seg + nb);
         const int slot = w - L.owner(seg);
         // the segment's first piece records how many pieces it has
         if (slot == 0 && p.ws_np && tid == 0) p.ws_np[s * gy + by] = L.owner(seg + nb - 1) - w + 1;
-        split(s, by, len, (int)(64 * (cur - seg)), min((int)(64 * (pend - seg)), len), slot,
+        split(s, by, len, tb.row0(p, s), 64 * (cur - seg), min(64 * (pend - seg), len), slot,
               cur == seg && pend == seg + nb);
         // the next piece reuses the LDS buffers and counters
         __syncthreads();
