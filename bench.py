@@ -401,6 +401,7 @@ def ptrace_summary(args):
             "config": name, "waves": int(len(w)),
             "shader_clock_GHz": {"median": round(q(ghz, 50), 3), "p10": round(q(ghz, 10), 3), "p90": round(q(ghz, 90), 3)},
             "loop_cycles_per_chunk": round(q(w[:, 0] / chunks, 50), 1),
+            "exact_path_chunk_frac": round(float((raw[keep][:, 3] >> np.uint64(32)).astype(np.float64).sum() / chunks.sum()), 4),
             "tile_wait_frac": round(float(w[:, 1].sum() / w[:, 0].sum()), 4),
             "barrier_frac": round(float(w[:, 2].sum() / w[:, 0].sum()), 4),
             "entry_to_loop_us": round(q((w[:, 5] - w[:, 4]) / 100.0, 50), 2),
