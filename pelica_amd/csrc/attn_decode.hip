@@ -626,22 +626,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
                 }
             }
     };
-    // EARLY_V (head dim 64: 32 more VGPRs fit): the block's V^T operands are
-    // read before the softmax and after_vreads() then runs (the V buffer is
-    // free for the next block's loads before the softmax, not after PV)
-    auto softmax_pv = [&](int kb, auto&& after_vreads) {
+    // The softmax needs only the scores: it runs before wait_v() (the wait
+    // for the block's V), while V is still arriving.  EARLY_V (head dim 64:
+    // 32 more VGPRs fit): the block's V^T operands are then all read and
+    // after_vreads() runs before the PV MFMAs (the V buffer is free for the
+    // next block's loads before PV, not after it).
+    auto softmax_pv = [&](int kb, auto&& wait_v, auto&& after_vreads) {
         const _Float16* vb = reinterpret_cast<const _Float16*>(vlds);
-        half8 va_all[EARLY_V ? 2 : 1][DT];
-        if constexpr (EARLY_V) {
-#pragma unroll
-            for (int u = 0; u < 2; ++u)
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) {
-                    const int k0 = 32 * u + 4 * g + (c16 >> 2), d0 = 16 * dt + 4 * (c16 & 3);
-                    va_all[u][dt] = cat8(lds_read_tr(v_elem<HD>(vb, k0, d0)), lds_read_tr(v_elem<HD>(vb, k0 + 16, d0)));
-                }
-            after_vreads();
-        }
         // mask (blocks at a range boundary only): row r sees keys [lor, posr]
         if (kb < lo_hi || kb + 63 > pos_lo) {
 #pragma unroll
@@ -687,6 +678,18 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) o[dt][rt] *= c;
         }
+        wait_v();
+        half8 va_all[EARLY_V ? 2 : 1][DT];
+        if constexpr (EARLY_V) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    const int k0 = 32 * u + 4 * g + (c16 >> 2), d0 = 16 * dt + 4 * (c16 & 3);
+                    va_all[u][dt] = cat8(lds_read_tr(v_elem<HD>(vb, k0, d0)), lds_read_tr(v_elem<HD>(vb, k0 + 16, d0)));
+                }
+            after_vreads();
+        }
         // O^T += V^T P^T; the dim tiles are independent accumulators
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
@@ -724,13 +727,17 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
             wait_lgkm0();
             if (i + 1 < nb) issue_k(i + 1, false);
         });
-        if (i + 1 < nb) wait_vm<VPL>();  // V(i) landed
-        else wait_vm<0>();
-        if (i < 2) DTRACE(2 + i);
-        softmax_pv(blk(i), [&] {
-            wait_lgkm0();
-            if (i + 1 < nb) issue_v(i + 1, false);
-        });
+        softmax_pv(
+            blk(i),
+            [&] {
+                if (i + 1 < nb) wait_vm<VPL>();  // V(i) landed
+                else wait_vm<0>();
+                if (i < 2) DTRACE(2 + i);
+            },
+            [&] {
+                wait_lgkm0();
+                if (i + 1 < nb) issue_v(i + 1, false);
+            });
         if constexpr (!EARLY_V) {
             wait_lgkm0();
             if (i + 1 < nb) issue_v(i + 1, false);
