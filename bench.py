@@ -31,8 +31,8 @@ F16_PEAK_TFLOPS = 2500.0    # MI355X dense f16 MFMA
 # dispatch), FETCH_SIZE scaled by 2.0: on this GPU it reads half the bytes a
 # plain copy of known size moves, while WRITE_SIZE reads them exactly
 # (profiles/hbm_traffic_counters.md).
-HBM_TRAFFIC_C3 = 69_734_605   # 32898.1 KiB fetched (x2) + 2304.0 KiB written per split launch
-HBM_TRAFFIC_C4 = 78_346_650   # 21871.2 KiB fetched (x2) + 32768 KiB written per prefill launch
+HBM_TRAFFIC_C3 = 69_744_435   # 32902.9 KiB fetched (x2) + 2304.0 KiB written per split launch
+HBM_TRAFFIC_C4 = 77_148_979   # 21286.4 KiB fetched (x2) + 32768 KiB written per prefill launch
 
 
 def parse():
