@@ -678,6 +678,17 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) o[dt][rt] *= c;
         }
+        // the softmax stays ahead of the wait for V (it needs only the
+        // scores): the empty asm takes P as an operand, so P is computed
+        // here; otherwise the compiler sinks the exp2s below the wait
+        if constexpr (EARLY_V) {
+#pragma unroll
+            for (int pp = 0; pp < NP; ++pp)
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) __asm__ volatile("" : "+v"(pf[pp][rt][u]));
+        }
         wait_v();
         half8 va_all[EARLY_V ? 2 : 1][DT];
         if constexpr (EARLY_V) {
