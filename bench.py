@@ -390,6 +390,9 @@ def ptrace_summary(args):
         rc = lib.pelica_attn_debug_ptrace(buf.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(buf.nbytes))
         assert rc == 0, rc
         raw = buf.reshape(-1, 16)
+        if (raw[:, 15] == 1).any():
+            slide_summary(name, raw)
+            continue
         n_chunks = raw[:, 3] & np.uint64(0xFFFFFFFF)
         keep = (raw[:, 7] > 0) & (n_chunks > 0)  # waves of the grid that ran the loop
         w = raw[keep].astype(np.float64)
@@ -415,6 +418,34 @@ def ptrace_summary(args):
             "loop_us": round(q(loop_us, 50), 2),
             "loop_to_exit_us": round(q((w[:, 7] - w[:, 6]) / 100.0, 50), 2),
         }), flush=True)
+
+
+def slide_summary(name, raw):
+    """Timeline of the sliding-window prefill kernel (prefill_slide_kernel
+    stamps): us from the earliest wave entry, p10/p50/p90 over waves, and
+    per-wave compute time of the first block by wave index (waves 0-3 share
+    their SIMDs with waves 4-7)."""
+    import numpy as np
+
+    keep = raw[:, 7] > 0
+    w = raw[keep].astype(np.float64)
+    t0 = w[:, 4].min()
+    q3 = lambda a: [round(float(np.percentile(a, x)), 2) for x in (10, 50, 90)]
+    chunks = (raw[keep][:, 3] & np.uint64(0xFFFFFFFF)).astype(np.float64)
+    comp_us = (w[:, 9] - w[:, 8] + np.where(w[:, 11] > 0, w[:, 11] - w[:, 10], 0)) / 100.0
+    wg = raw[: len(raw) // 8 * 8].reshape(-1, 8, 16).astype(np.float64)
+    wg = wg[(wg[:, :, 7] > 0).all(axis=1)]
+    b0 = (wg[:, :, 9] - wg[:, :, 8]) / 100.0
+    out = {"config": name, "kernel": "prefill_slide_kernel", "waves": int(len(w)),
+           "shader_clock_GHz": q3(w[:, 0] / (comp_us * 1e3)),
+           "compute_cycles_per_chunk": q3(w[:, 0] / chunks),
+           "exact_path_chunk_frac": round(float((raw[keep][:, 3] >> np.uint64(32)).astype(np.float64).sum() / chunks.sum()), 4),
+           "block0_compute_us_by_wave": [round(float(np.median(b0[:, k])), 2) for k in range(8)]}
+    for key, col in [("first_compute", 5), ("block0_end", 9), ("block1_barrier", 12), ("block1_queries_read", 13),
+                     ("block0_output_stored", 14), ("block1_start", 10), ("block1_end", 11), ("exit", 7)]:
+        if (w[:, col] > 0).any():
+            out[key + "_us"] = q3((w[w[:, col] > 0][:, col] - t0) / 100.0)
+    print(json.dumps(out), flush=True)
 
 
 def dtrace_summary(args):

@@ -24,6 +24,7 @@
 // (src/oss_prefill.rs:408).  Workgroups are ordered so that each XCD works on
 // one kv head (its K/V stays in that XCD's L2) and the longest key ranges
 // start first.
+#include <algorithm>
 #include <type_traits>
 
 #include "attn_prefill.hpp"
@@ -671,6 +672,458 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
         g_ptrace[wid * 16 + 8] = rt_issued;
         g_ptrace[wid * 16 + 9] = rt_landed;
         g_ptrace[wid * 16 + 10] = rt_bar;
+        g_ptrace[wid * 16 + 15] = 0;  // (this kernel's layout)
+    }
+#endif
+}
+
+// Sliding-window prefill over consecutive token blocks (head dim 64, 8
+// heads per kv head, windows up to 130 keys).  One 8-wave workgroup per CU
+// takes `spw` consecutive 64-token blocks of one kv head.  Keys sit in LDS
+// as a ring of 32-key chunks (slot = chunk mod NCH): consecutive blocks
+// share all but their last two chunks, so a block brings in two new chunks
+// (8 KB of K and V) and its queries, both requested while the block before
+// it is computed — its queries through the wave's own 8 KB staging area,
+// which also stages that wave's output rows.  Each wave walks only the
+// chunks its 8 tokens see (5 or 6); chunks are resident, so the chunk loop
+// has no waits or barriers; one barrier per block hands the ring over.
+// The chunk step is the one of prefill_kernel (same pipeline, same lazy
+// softmax), with ring addresses in place of tile buffers.
+template <int NCH>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_slide_kernel(
+    PrefillParams p, int n_parts, int spw) {
+    constexpr int HD = 64, RT = 2, NW = 8, KS = HD / 16, DT = HD / 32, PPR = HD / 8, HPK = 8;
+    constexpr int CHB = 32 * HD * 2;            // bytes of a 32-key chunk of K (or V)
+    constexpr int OUT_WAVE = RT * 32 * HD * 2;  // bytes of one wave's rows (queries in, output out)
+    constexpr int TBK = NW * RT * 32 / HPK;     // tokens per block (64)
+    __shared__ __attribute__((aligned(16))) char lds[2 * NCH * CHB + CHB + NW * OUT_WAVE];
+    char* const kring = lds;
+    char* const vring = lds + NCH * CHB;
+    char* const vzero = lds + 2 * NCH * CHB;  // the (empty) PV of chunk -1 reads zeros
+
+    const int nblk = gridDim.x;
+    int bid = blockIdx.x;
+    if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);  // one kv head per XCD
+    const int part = bid % n_parts, rest = bid / n_parts;
+    const int kvh = rest % p.n_kv, s = rest / p.n_kv;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, h2 = lane >> 5,
+              c32 = lane & 31;
+    char* const stage = vzero + CHB + wave * OUT_WAVE;
+#ifdef PELICA_PTRACE
+    // stamps (prefill_kernel's layout where they mean the same): [0]
+    // compute cycles, [1] block-top wait cycles, [2] barrier cycles, [3]
+    // exact-path chunks << 32 | chunks, [4] entry, [5] first compute start,
+    // [6] last compute end, [7] exit, [8] + 2 k / [9] + 2 k: compute start /
+    // end of the workgroup's block k (k < 3), for block 1: [12] barrier
+    // passed, [13] queries read, [14] previous output stored; [15] = 1
+    // (this kernel's layout)
+    const unsigned long long rt_entry = rtime();
+    unsigned t_comp = 0, t_wait = 0, t_bar = 0, n_ch_all = 0, n_exact = 0;
+    unsigned long long rt_first = 0, rt_last = 0;
+    const int wid = blockIdx.x * 8 + (threadIdx.x >> 6);
+#endif
+    // the lane index through an empty asm: per-block address arithmetic
+    // derived from it is recomputed where it is used instead of being
+    // hoisted out of the block loop (where it would hold ~40 VGPRs)
+    auto fresh_lane = [&] {
+        int ln = lane;
+        __asm__ volatile("" : "+v"(ln));
+        return ln;
+    };
+
+    const int len = seq_keys(p.seq_len, s, p.kv_len);
+    if (len < p.T || len <= 0) return;
+    const int n_steps = (p.T + TBK - 1) / TBK;
+    const int j0 = part * spw, j1 = min(j0 + spw, n_steps);
+    if (j0 >= j1) return;
+    const int64_t row0 = p.seq_off ? p.seq_off[s] : (int64_t)s * p.kv_len;
+    const int qoff0 = len - p.T;  // position of token 0
+    const uint32_t stride_b = (uint32_t)p.row_stride * 2;
+    const uint32_t nrec = (uint32_t)len * stride_b;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.k + row0 * p.row_stride + (size_t)kvh * HD), (short)0, (int)nrec, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.v + row0 * p.row_stride + (size_t)kvh * HD), (short)0, (int)nrec, kBufferFlags);
+    const uint32_t qtok_b = (uint32_t)p.n_head * HD * 2;  // bytes of one token's query heads
+    auto q_rsrc = [&](int j) {
+        const int t0 = j * TBK, t1 = min(t0 + TBK, p.T);
+        return __builtin_amdgcn_make_buffer_rsrc((void*)(p.q + ((size_t)s * p.T + t0) * p.n_head * HD), (short)0,
+                                                 (int)((uint32_t)(t1 - t0) * qtok_b), kBufferFlags);
+    };
+    // chunks [first, last] of block j: keys a row of the block sees
+    auto chunk_lo = [&](int j) { return max(0, qoff0 + j * TBK + 1 - p.window) >> 5; };
+    auto chunk_hi = [&](int j) { return (qoff0 + min(j * TBK + TBK, p.T) - 1) >> 5; };
+    auto slot = [](int c) { return c % NCH; };
+    // chunk c into its ring slot: waves 0-3 bring its K, 4-7 its V (one
+    // 16-byte piece per lane; the lane loads the logical piece its slot holds)
+    auto load_chunk = [&](int c, bool tracked) {
+        const int lane = fresh_lane();
+        const bool is_v = wave >= 4;
+        const int q = 64 * (wave & 3) + lane, key = q / PPR, phys = q % PPR;
+        const int piece = is_v ? phys ^ ((key & 3) << 1) : phys ^ (key & 7);
+        const uint32_t off = (uint32_t)(32 * c + key) * stride_b + 16 * piece;
+        char* const dst = (is_v ? vring : kring) + slot(c) * CHB + 1024 * (wave & 3);
+        if (tracked) lds_dma16(is_v ? rv : rk, off, dst);
+        else lds_dma16_untracked(is_v ? rv : rk, off, dst);
+    };
+    // the wave's query rows of block j into its staging area: instruction i
+    // brings token 8 wave + i (its 8 heads, 1 KB), row 8 i + lane / 8, the
+    // row's 16-byte pieces swizzled by its low 3 bits
+    auto load_q_stage = [&](int j) {
+        const __amdgpu_buffer_rsrc_t rq = q_rsrc(j);
+        const int lane = fresh_lane(), hr = lane / PPR, phys = lane % PPR;
+#pragma unroll
+        for (int i = 0; i < RT * 32 / HPK; ++i) {
+            const int row = HPK * i + hr;
+            const uint32_t off = (uint32_t)(HPK * wave + i) * qtok_b + (uint32_t)((kvh * HPK + hr) * HD) * 2 +
+                                 16 * (phys ^ (row & 7));
+            lds_dma16_untracked(rq, off, stage + 1024 * i);
+        }
+    };
+
+    static_assert(CHB / 16 <= 64 * NW, "one zero store per thread");
+    if (tid < CHB / 16) *reinterpret_cast<u32x4*>(vzero + 16 * tid) = u32x4{0, 0, 0, 0};
+    // first block's chunks, then its queries straight into registers
+    for (int c = chunk_lo(j0); c <= chunk_hi(j0); ++c) load_chunk(c, true);
+    half8 qb[RT][KS];
+    {
+        const __amdgpu_buffer_rsrc_t rq = q_rsrc(j0);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            const int r = (wave * RT + rt) * 32 + c32;
+            const uint32_t qoff = (uint32_t)(r / HPK) * qtok_b + (uint32_t)((kvh * HPK + r % HPK) * HD + 8 * h2) * 2;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+                qb[rt][ks] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + 32 * ks, 0, 0));
+        }
+    }
+    float sk[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const int r = (wave * RT + rt) * 32 + c32;
+        sk[rt] = p.sinks ? p.sinks[kvh * HPK + r % HPK] * kLog2e : 0.f;
+    }
+
+    float m[RT], l[RT];
+    float16v o[DT][RT];
+    int posr[RT], lor[RT];
+    bool valid[RT];
+    int c0 = 0;  // the wave's first chunk of the current block
+    const half2 one2 = {(_Float16)1.f, (_Float16)1.f};
+    constexpr float kSumLimit = 16384.f;
+
+    // the wave's normalised rows of block j -> staging area -> whole rows out
+    auto store_out = [&](int j) {
+        const int t0 = j * TBK, t1 = min(t0 + TBK, p.T);
+        const int lane = fresh_lane(), c32 = lane & 31, h2 = lane >> 5;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            const float inv = 1.f / half_sum(l[rt]);
+            const int rl = rt * 32 + c32;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    const half4 hv = {(_Float16)(o[dt][rt][4 * i4] * inv), (_Float16)(o[dt][rt][4 * i4 + 1] * inv),
+                                      (_Float16)(o[dt][rt][4 * i4 + 2] * inv), (_Float16)(o[dt][rt][4 * i4 + 3] * inv)};
+                    const int pc = 4 * dt + i4;
+                    *reinterpret_cast<half4*>(stage + rl * (HD * 2) + ((pc ^ (rl % PPR)) << 4) + 8 * h2) = hv;
+                }
+        }
+        // every row read back first, then the stores through a buffer
+        // resource over the block's output rows (rows past the prompt fall
+        // outside it and are dropped: no branch per store)
+        constexpr int RPI = 64 / PPR;
+        constexpr int NST = RT * 32 / RPI;
+        const int pc = lane % PPR;
+        u32x4 val[NST];
+#pragma unroll
+        for (int k = 0; k < NST; ++k) {
+            const int rl = k * RPI + lane / PPR;
+            val[k] = *reinterpret_cast<const u32x4*>(stage + rl * (HD * 2) + ((pc ^ (rl % PPR)) << 4));
+        }
+        const uint32_t otok_b = (uint32_t)p.n_head * HD * 2;
+        const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(p.out + ((size_t)s * p.T + t0) * p.n_head * HD), (short)0, (int)((uint32_t)(t1 - t0) * otok_b),
+            kBufferFlags);
+#pragma unroll
+        for (int k = 0; k < NST; ++k) {
+            const int r = wave * RT * 32 + k * RPI + lane / PPR;  // token r / HPK of the block, head r % HPK
+            const uint32_t off = (uint32_t)(r / HPK) * otok_b + (uint32_t)((kvh * HPK + r % HPK) * HD + 8 * pc) * 2;
+            __builtin_amdgcn_raw_buffer_store_b128(val[k], ro, off, 0, 0);
+        }
+    };
+
+    // S^T of chunk c (wave-local index) into sc
+    auto qk = [&](int c, float16v (&sc)[RT]) {
+        const char* kt = kring + slot(c0 + c) * CHB;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) sc[rt] = float16v{};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const half8 ka = *reinterpret_cast<const half8*>(kt + k_slot<HD>(c32, 2 * ks + h2));
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) sc[rt] = mfma32(ka, qb[rt][ks], sc[rt]);
+        }
+    };
+    auto pv = [&](int c, const half8 (&pb)[2][RT]) {
+        const char* vt = vring + slot(c0 + c) * CHB;
+        const int G = lane >> 4, r4 = (lane & 15) >> 2, q4 = lane & 3;
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            half8 va[DT];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const int key = 16 * w + 4 * h2 + r4, dim = 32 * dt + 16 * (G & 1) + 4 * q4;
+                const _Float16* a0 = reinterpret_cast<const _Float16*>(vt + v_slot<HD>(key, dim >> 3) + ((dim & 7) << 1));
+                const _Float16* a1 = reinterpret_cast<const _Float16*>(vt + v_slot<HD>(key + 8, dim >> 3) + ((dim & 7) << 1));
+                va[dt] = cat8(lds_read_tr(a0), lds_read_tr(a1));
+            }
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) o[dt][rt] = mfma32(va[dt], pb[w][rt], o[dt][rt]);
+        }
+    };
+
+    float16v s_a[RT], s_b[RT];
+    half8 p_a[2][RT], p_b[2][RT];
+    int wpf = 0, wlo_last = 0;  // the wave's first row position and last row's window start
+
+    // one chunk: prefill_kernel's step with ring addresses
+    auto step = [&](int c, float16v (&s_cur)[RT], float16v (&s_nxt)[RT], const half8 (&p_prv)[2][RT],
+                    half8 (&p_cur)[2][RT]) {
+        const int kb = 32 * (c0 + c);
+        if (kb + 31 > wpf || kb < wlo_last) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int key = kb + 8 * (i / 4) + 4 * h2 + (i % 4);
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt)
+                    if (key < lor[rt] || key > posr[rt]) s_cur[rt][i] = -INFINITY;
+            }
+        }
+        constexpr int NOPD = KS + 2 * DT;
+        half8 opd[NOPD];
+        const char* const kt_c = kring + slot(c0 + c + 1) * CHB;  // (past the last chunk: discarded)
+        const char* const vt_c = c == 0 ? vzero : vring + slot(c0 + c - 1) * CHB;
+        auto read_opd = [&](int r) {
+            if (r < KS) {
+                opd[r] = *reinterpret_cast<const half8*>(kt_c + k_slot<HD>(c32, 2 * r + h2));
+            } else {
+                const int w = (r - KS) / DT, dt = (r - KS) % DT;
+                const int G = lane >> 4, r4 = (lane & 15) >> 2, q4 = lane & 3;
+                const int key = 16 * w + 4 * h2 + r4, dim = 32 * dt + 16 * (G & 1) + 4 * q4;
+                const _Float16* a0 = reinterpret_cast<const _Float16*>(vt_c + v_slot<HD>(key, dim >> 3) + ((dim & 7) << 1));
+                const _Float16* a1 = reinterpret_cast<const _Float16*>(vt_c + v_slot<HD>(key + 8, dim >> 3) + ((dim & 7) << 1));
+                opd[r] = cat8(lds_read_tr(a0), lds_read_tr(a1));
+            }
+        };
+        read_opd(0);
+        read_opd(1);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) s_nxt[rt] = float16v{};
+        constexpr int NM = KS * RT + 2 * DT * RT;
+        constexpr int NS = 16 * RT;
+        constexpr int NP = NS / 2;
+        static_assert(NS % NM == 0, "whole scores per MFMA slot");
+        constexpr int S = NS / NM;
+        float ms[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) ms[rt] = m[rt] == -INFINITY ? 0.f : m[rt];
+        float acc[RT][2];
+        float e[NS];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) acc[rt][0] = acc[rt][1] = 0.f;
+        auto op_fma = [&](int i) {
+            if (i < NS) s_cur[i / 16][i % 16] = __builtin_fmaf(s_cur[i / 16][i % 16], p.qscale, -ms[i / 16]);
+        };
+        auto op_exp = [&](int i) {
+            if (i < NS) e[i] = fast_exp2(s_cur[i / 16][i % 16]);
+        };
+        auto op_pack = [&](int k) {
+            const int rt = k / 8, i = 2 * (k % 8);
+            p_cur[i / 8][rt][i % 8] = (_Float16)e[2 * k];
+            p_cur[i / 8][rt][i % 8 + 1] = (_Float16)e[2 * k + 1];
+        };
+        auto op_dot = [&](int k) {
+            const int rt = k / 8, i = 2 * (k % 8);
+            acc[rt][k & 1] = __builtin_amdgcn_fdot2(half2{p_cur[i / 8][rt][i % 8], p_cur[i / 8][rt][i % 8 + 1]}, one2,
+                                                    acc[rt][k & 1], false);
+        };
+        auto packable = [](int u) { return u < 0 ? 0 : (S * (u + 1)) / 2; };
+#pragma unroll
+        for (int j = 0; j < S; ++j) op_fma(j);
+#pragma unroll
+        for (int t = 0; t < NM; ++t) {
+            const int r = t / RT;
+            if (t % RT == 0 && r + 2 < NOPD) read_opd(r + 2);
+            if (t < KS * RT) {
+                const int rt = t % RT;
+                s_nxt[rt] = mfma32(opd[r], qb[rt][r], s_nxt[rt]);
+            } else {
+                const int j = t - KS * RT, w = j / (DT * RT), dt = (j / RT) % DT, rt = j % RT;
+                o[dt][rt] = mfma32(opd[r], p_prv[w][rt], o[dt][rt]);
+            }
+#pragma unroll
+            for (int k = packable(t - 3); k < packable(t - 2); ++k) op_dot(k);
+#pragma unroll
+            for (int k = packable(t - 2); k < packable(t - 1); ++k) op_pack(k);
+#pragma unroll
+            for (int j = 0; j < S; ++j) op_exp(S * t + j);
+#pragma unroll
+            for (int j = 0; j < S; ++j) op_fma(S * (t + 1) + j);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int k = packable(NM - 2); k < NP; ++k) op_pack(k);
+#pragma unroll
+        for (int k = packable(NM - 3); k < NP; ++k) op_dot(k);
+        float ls[RT];
+        bool bad = false;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            ls[rt] = acc[rt][0] + acc[rt][1];
+            bad |= !(ls[rt] <= kSumLimit) || m[rt] == -INFINITY;
+        }
+#ifdef PELICA_PTRACE
+        n_exact += __builtin_amdgcn_ballot_w64(bad) != 0;
+#endif
+        if (__builtin_amdgcn_ballot_w64(bad)) {
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                float x = -INFINITY;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) x = fmaxf(x, s_cur[rt][i]);
+                const float mn = fmaxf(m[rt], half_max(x) + ms[rt]);
+                if (mn > m[rt]) {
+                    const float cf = fast_exp2(m[rt] - mn);
+                    l[rt] *= cf;
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt) o[dt][rt] *= cf;
+                    m[rt] = mn;
+                }
+                const float shift = ms[rt] - (m[rt] == -INFINITY ? 0.f : m[rt]);
+                float a = 0.f;
+#pragma unroll
+                for (int w = 0; w < 2; ++w)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        p_cur[w][rt][j] = (_Float16)fast_exp2(s_cur[rt][8 * w + j] + shift);
+                        a += (float)p_cur[w][rt][j];
+                    }
+                ls[rt] = a;
+            }
+        }
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) l[rt] += ls[rt];
+    };
+
+    for (int j = j0; j < j1; ++j) {
+        const int t0 = j * TBK, t1 = min(t0 + TBK, p.T);
+
+        // The loads of block j (chunks and, after the first block, queries)
+        // have landed, and every wave is done with block j-1's chunks.
+#ifdef PELICA_PTRACE
+        const unsigned ta = cyc();
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        const unsigned tb2 = cyc();
+        __syncthreads();
+        t_wait += tb2 - ta;
+        t_bar += cyc() - tb2;
+        if (lane == 0 && j == j0 + 1) g_ptrace[wid * 16 + 12] = rtime();
+#else
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __syncthreads();
+#endif
+        if (j > j0) {
+            // block j's queries from the staging area, then block j-1's
+            // output through it (a wave's LDS accesses complete in order)
+            const int lane = fresh_lane(), c32 = lane & 31, h2 = lane >> 5;
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const int rl = rt * 32 + c32;
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+                    qb[rt][ks] = *reinterpret_cast<const half8*>(stage + rl * (HD * 2) + (((2 * ks + h2) ^ (rl & 7)) << 4));
+            }
+#ifdef PELICA_PTRACE
+            if (lane == 0 && j == j0 + 1) g_ptrace[wid * 16 + 13] = rtime();
+#endif
+            store_out(j - 1);
+#ifdef PELICA_PTRACE
+            if (lane == 0 && j == j0 + 1) g_ptrace[wid * 16 + 14] = rtime();
+#endif
+        }
+        // block j+1's new chunks and queries, in flight while j is computed
+        if (j + 1 < j1) {
+            for (int c = chunk_hi(j) + 1; c <= chunk_hi(j + 1); ++c) load_chunk(c, false);
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the staging area's reads are done
+            load_q_stage(j + 1);
+        }
+        // this wave's rows of block j: tokens t0 + 8 wave .. + 7
+        const int tw0 = t0 + RT * 32 / HPK * wave;
+        const int tw1 = min(tw0 + RT * 32 / HPK, t1);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            const int r = (wave * RT + rt) * 32 + c32;
+            const int t = t0 + r / HPK;
+            valid[rt] = t < t1;
+            posr[rt] = valid[rt] ? qoff0 + t : -1;
+            lor[rt] = (posr[rt] + 1 > p.window) ? posr[rt] + 1 - p.window : 0;
+            m[rt] = valid[rt] ? (p.sinks ? sk[rt] : -INFINITY) : 0.f;
+            l[rt] = (valid[rt] && p.sinks && h2 == 0) ? 1.f : 0.f;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o[dt][rt] = float16v{};
+        }
+        if (tw0 >= tw1) continue;  // (no rows: past the prompt)
+        wpf = qoff0 + tw0;
+        const int wpl = qoff0 + tw1 - 1;
+        wlo_last = max(0, wpl + 1 - p.window);
+        c0 = max(0, wpf + 1 - p.window) >> 5;
+        const int nch = (wpl >> 5) - c0 + 1;
+#pragma unroll
+        for (int w = 0; w < 2; ++w)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) p_b[w][rt] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+#ifdef PELICA_PTRACE
+        const unsigned tc0 = cyc();
+        {
+            const unsigned long long r0 = rtime();
+            if (j == j0) rt_first = r0;
+            if (lane == 0 && j - j0 < 3) g_ptrace[wid * 16 + 8 + 2 * (j - j0)] = r0;
+        }
+        n_ch_all += nch;
+#endif
+        qk(0, s_a);
+        // every chunk unrolled (a wave sees at most 6: 8 tokens under a
+        // window of up to 130 keys)
+        step(0, s_a, s_b, p_b, p_a);
+        if (nch > 1) step(1, s_b, s_a, p_a, p_b);
+        if (nch > 2) step(2, s_a, s_b, p_b, p_a);
+        if (nch > 3) step(3, s_b, s_a, p_a, p_b);
+        if (nch > 4) step(4, s_a, s_b, p_b, p_a);
+        if (nch > 5) step(5, s_b, s_a, p_a, p_b);
+        if (nch & 1) pv(nch - 1, p_a);
+        else pv(nch - 1, p_b);
+#ifdef PELICA_PTRACE
+        t_comp += cyc() - tc0;
+        rt_last = rtime();
+        if (lane == 0 && j - j0 < 3) g_ptrace[wid * 16 + 9 + 2 * (j - j0)] = rt_last;
+#endif
+    }
+    store_out(j1 - 1);
+#ifdef PELICA_PTRACE
+    if (lane == 0) {
+        g_ptrace[wid * 16 + 0] = t_comp;
+        g_ptrace[wid * 16 + 1] = t_wait;
+        g_ptrace[wid * 16 + 2] = t_bar;
+        g_ptrace[wid * 16 + 3] = (unsigned long long)n_exact << 32 | n_ch_all;
+        g_ptrace[wid * 16 + 4] = rt_entry;
+        g_ptrace[wid * 16 + 5] = rt_first;
+        g_ptrace[wid * 16 + 6] = rt_last;
+        g_ptrace[wid * 16 + 7] = rtime();
+        g_ptrace[wid * 16 + 15] = 1;
     }
 #endif
 }
@@ -717,8 +1170,48 @@ static hipError_t launch_nw(const PrefillParams& p, hipStream_t st) {
 // LDS serves twice the rows; the 4096-token gpt-oss causal prefill ~2 %
 // faster) unless a short window makes the larger token block mostly masked
 // (window 128: 4 waves, 25 % faster than 8).
+// ring slots of the sliding-window kernel: the chunks of two consecutive
+// 64-token blocks, (126 + window) / 32 + 2, fit for windows up to 130
+constexpr int kSlideChunks = 10;
+#ifdef PELICA_PRE_NO_SLIDE
+constexpr bool kNoSlide = true;
+#else
+constexpr bool kNoSlide = false;
+#endif
+
+static int prefill_cus() {
+    static const int n = [] {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        return cus;
+    }();
+    return n;
+}
+
+// the sliding-window kernel's shapes: head dim 64, 8 heads per kv head,
+// linear caches, whole-prompt launches, a window the ring holds
+static bool slide_fits(const PrefillParams& p) {
+    return !kNoSlide && p.hd == 64 && p.hpk == 8 && !p.ring_cap && !p.state && p.window > 0 &&
+           (126 + p.window) / 32 + 2 <= kSlideChunks;
+}
+
+static hipError_t launch_slide(const PrefillParams& p, hipStream_t st) {
+    const int n_steps = (p.T + 63) / 64;
+    const long long total = (long long)n_steps * p.n_kv * p.n_seq;
+    const int spw = (int)std::max(1LL, (total + prefill_cus() - 1) / prefill_cus());
+    const int n_parts = (n_steps + spw - 1) / spw;
+    const long long nblk = (long long)n_parts * p.n_kv * p.n_seq;
+    if (nblk > 0x7fffffff) return hipErrorNotSupported;
+    ProfScope ps(kProfPrefill, st);
+    hipLaunchKernelGGL((prefill_slide_kernel<kSlideChunks>), dim3((unsigned)nblk), dim3(512), 0, st, p, n_parts, spw);
+    return hipGetLastError();
+}
+
 template <int HD, int RT>
 static hipError_t launch(const PrefillParams& p, hipStream_t st) {
+    if (HD == 64 && RT == 2 && slide_fits(p)) return launch_slide(p, st);
     if (p.window > 0 && p.window <= 1024) return launch_nw<HD, RT, 4>(p, st);
     return launch_nw<HD, RT, 8>(p, st);
 }

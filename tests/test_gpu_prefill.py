@@ -114,3 +114,39 @@ def test_all_logits_far_below_zero(logit):
     got = gpu_run(inp)
     ref = oracle_run(inp)
     assert_close(as_f64(got), as_f64(ref), what=f"logit {logit}")
+
+
+# Sliding-window shapes the persistent ring kernel takes (head dim 64, 8
+# heads per kv head, window <= 130, linear cache): prompts after a cached
+# prefix, no sinks, prompts that end inside a 64-token block, several
+# sequences, and blocks per workgroup from 1 to 4.
+@pytest.mark.parametrize("T,L,window,sinks,n_seq", [
+    (300, 1200, 128, False, 1),    # after a prefix, no sinks (exact path first)
+    (65, 65, 128, True, 1),        # one full block and one token
+    (4096, 4096, 100, True, 1),    # two blocks per workgroup
+    (8192, 8192, 130, True, 1),    # four blocks per workgroup, widest ring span
+    (200, 900, 33, True, 3),       # several sequences with ragged prefixes
+])
+def test_slide_window(T, L, window, sinks, n_seq):
+    ragged = (T, L) if n_seq > 1 else None
+    cfg = wl.AttnConfig("pslide", "prefill", 64, 8, 64, L, q_tokens=T, window=window, sinks=sinks, n_seq=n_seq,
+                        ragged=ragged, seed=90 + window + T)
+    inp = wl.make_inputs(cfg, "cuda")
+    print(f"[case] slide window T{T} L{L} W{window} sinks{sinks} seqs{n_seq}", flush=True)
+    assert_close(as_f64(gpu_run(inp)), as_f64(oracle_run(inp)), what=f"slide T{T} W{window}")
+
+
+def test_slide_window_logits_far_below_zero():
+    # uniform scores far below 0, no sinks, under a window: each row's output
+    # is the mean of V over its window
+    T, L, hd, W = 300, 700, 64, 128
+    cfg = wl.AttnConfig("negw", "prefill", 64, 8, hd, L, q_tokens=T, window=W, seed=32)
+    inp = wl.make_inputs(cfg, "cuda")
+    k0 = torch.randn(hd, device="cuda")
+    k0 = k0 / k0.norm() * 4.0
+    inp.k.copy_(k0.half().expand_as(inp.k))
+    kf = inp.k[0, 0].float()
+    qv = kf * (-120.0 * np.sqrt(hd) / float(kf @ kf))
+    inp.q.copy_(qv.half().expand_as(inp.q))
+    print("[case] slide window logit -120", flush=True)
+    assert_close(as_f64(gpu_run(inp)), as_f64(oracle_run(inp)), what="slide window logit -120")
