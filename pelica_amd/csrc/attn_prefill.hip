@@ -609,16 +609,30 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
                 }
         }
         // (a wave's LDS accesses complete in order: it reads its own rows)
+        // Every row is read back first, then stored through a buffer
+        // resource over the block's output tokens: rows past the block fall
+        // outside it (offset past num_records) and are dropped, no branch
+        // per store.
         constexpr int RPI = 64 / PPR;  // rows per store instruction
+        constexpr int NST = RT * 32 / RPI;
         const int pc = lane % PPR;
+        u32x4 val[NST];
 #pragma unroll
-        for (int k = 0; k < RT * 32 / RPI; ++k) {
+        for (int k = 0; k < NST; ++k) {
             const int rl = k * RPI + lane / PPR;
-            const u32x4 val = *reinterpret_cast<const u32x4*>(ow + rl * (HD * 2) + ((pc ^ (rl % PPR)) << 4));
-            const int r = wave * RT * 32 + rl;
-            const int t = t0 + r / p.hpk, h = kvh * p.hpk + r % p.hpk;
-            if (r < TB * p.hpk && t < t1)
-                *reinterpret_cast<u32x4*>(p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + 8 * pc) = val;
+            val[k] = *reinterpret_cast<const u32x4*>(ow + rl * (HD * 2) + ((pc ^ (rl % PPR)) << 4));
+        }
+        const uint32_t otok_b = (uint32_t)p.n_head * HD * 2;
+        const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(p.out + ((size_t)s * p.T + t0) * p.n_head * HD), (short)0, (int)((uint32_t)(t1 - t0) * otok_b),
+            kBufferFlags);
+#pragma unroll
+        for (int k = 0; k < NST; ++k) {
+            const int r = wave * RT * 32 + k * RPI + lane / PPR;
+            const uint32_t off = r < TB * p.hpk ? (uint32_t)(r / p.hpk) * otok_b +
+                                                      (uint32_t)((kvh * p.hpk + r % p.hpk) * HD + 8 * pc) * 2
+                                                : 0xFFFFFF00u;  // (rows past the block's token count)
+            __builtin_amdgcn_raw_buffer_store_b128(val[k], ro, off, 0, 0);
         }
     } else {
     // O^T lane layout: dim 32 dt + 8 (i / 4) + 4 h2 + i % 4 of row c32
