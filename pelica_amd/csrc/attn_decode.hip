@@ -506,8 +506,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     // Load j of a block fills LDS slots j*64 + lane of the wave's buffer
     // (buffer_load ... lds).  K of a block is requested before its V, so
     // QK^T can start while V is still arriving.
-    // (block 0's loads are tracked by the compiler: the query loads below
-    // are waited for behind them; the loop's are not, see the loop)
+    // (block 0's loads are tracked by the compiler; the loop's are
+    // untracked, see the loop)
     auto issue_k = [&](int i, bool tracked) {
 #pragma unroll
         for (int j = 0; j < VPL; ++j)
@@ -517,12 +517,45 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
 #pragma unroll
         for (int j = 0; j < VPL; ++j) kv_dma16(rv, row_of(i, j) + vcol, vlds + 1024 * j, tracked);
     };
-    if (nb > 0) {
+    // ---- block 0 and this lane's queries ----
+    // Head dim 128: the queries are requested first (a few hundred bytes
+    // per wave), then block 0 — the wait for the queries then leaves K and V
+    // in flight, so QK^T starts when K lands, not once V has (measured:
+    // 32-sequence draft batch 108.6 -> 105.3-107.0 us, 8K-key GQA decode
+    // 11.5 -> 11.3 us; the 2K-key call's split kernel 7.75 -> 7.6 us, its
+    // whole call 10.45 -> 10.6 us).
+    // Head dim 64: block 0 first, the queries behind it (the next block's K
+    // then goes out only once V has landed; requested earlier, it delays
+    // that V and the whole stream: gpt-oss decode +0.4 us, and the 128-key
+    // window call +0.7 us).
+    constexpr bool QFIRST = HD == 128;
+    if (!QFIRST && nb > 0) {
+        issue_k(0, true);
+        issue_v(0, true);
+    }
+    float4v qraw[RT][DS][2];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const int r = rbase + 16 * rt + (PK ? (c16 & 7) : c16);
+        const int rr = r < p.R ? r : 0;
+        const int t = rr / p.hpk, h = kvh * p.hpk + rr % p.hpk;
+        const float* qp = p.q + ((size_t)(s * p.T + t) * p.n_head + h) * HD + 8 * g;
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+            qraw[rt][ds][0] = *reinterpret_cast<const float4v*>(qp + 32 * ds);
+            qraw[rt][ds][1] = *reinterpret_cast<const float4v*>(qp + 32 * ds + 4);
+        }
+    }
+    // (issued even with no block: past num_records they read zeros without
+    // touching memory, and the compiler's wait for the queries is then the
+    // same count on every path; such a wave waits for them before its K/V
+    // buffer holds its state)
+    if (QFIRST) {
         issue_k(0, true);
         issue_v(0, true);
     }
 
-    // ---- queries of this lane's rows: f16 parts (hi[, lo]) in base 2 ----
+    // ---- f16 parts (hi[, lo]) of the queries in base 2 ----
     // PK: column c16 < 8 holds the hi part of row c16, column c16 + 8 its lo
     // part; the two partial scores are summed across lanes l, l ^ 8.
     half8 qf[NP][RT][DS];
@@ -533,8 +566,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
         const int r = rbase + 16 * rt + (PK ? (c16 & 7) : c16);
         const bool rv_ok = r < p.R;
         const int rr = rv_ok ? r : 0;
-        const int t = rr / p.hpk, h = kvh * p.hpk + rr % p.hpk;
-        const float* qp = p.q + ((size_t)(s * p.T + t) * p.n_head + h) * HD + 8 * g;
+        const int t = rr / p.hpk;
         const KeyRange krg = key_range(len, p.T, t, p.window);
         posr[rt] = rv_ok ? krg.pos : -1;
         lor[rt] = krg.lo;
@@ -544,8 +576,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
         }
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds) {
-            const float4v a = *reinterpret_cast<const float4v*>(qp + 32 * ds);
-            const float4v b = *reinterpret_cast<const float4v*>(qp + 32 * ds + 4);
+            const float4v a = qraw[rt][ds][0], b = qraw[rt][ds][1];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const float x = rv_ok ? (j < 4 ? a[j] : b[j - 4]) * p.qscale : 0.f;
@@ -754,6 +785,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
             if (i + 1 < nb) issue_v(i + 1, false);
         }
     }
+    if (QFIRST && nb == 0) wait_vm<0>();  // (block 0's zero reads: the buffers hold the state next)
     DTRACE(4);
     if (PK) {
         // columns c16 and c16 ^ 8 hold the hi and lo parts of one row
