@@ -527,7 +527,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     // Head dim 64: block 0 first, the queries behind it (the next block's K
     // then goes out only once V has landed; requested earlier, it delays
     // that V and the whole stream: gpt-oss decode +0.4 us, and the 128-key
-    // window call +0.7 us).
+    // window call +0.7 us; with the queries first and K(1) held back until
+    // V(0) has landed, gpt-oss decode is even and the window call +0.5 us).
     constexpr bool QFIRST = HD == 128;
     if (!QFIRST && nb > 0) {
         issue_k(0, true);
