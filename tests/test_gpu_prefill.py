@@ -126,6 +126,8 @@ def test_all_logits_far_below_zero(logit):
     (4096, 4096, 100, True, 1),    # two blocks per workgroup
     (8192, 8192, 130, True, 1),    # four blocks per workgroup, widest ring span
     (200, 900, 33, True, 3),       # several sequences with ragged prefixes
+    (1, 500, 128, True, 1),        # one token: seven waves without rows
+    (63, 63, 1, False, 1),         # a window of one key, no sinks
 ])
 def test_slide_window(T, L, window, sinks, n_seq):
     ragged = (T, L) if n_seq > 1 else None
