@@ -340,6 +340,12 @@ def profile_only(args):
                 attn.mla(q, lats[i % len(lats)], kv_len=32768)
             torch.cuda.synchronize()
             continue
+        if name == "qkv_rope_cache_gptoss_4096":  # (its timed graph replays)
+            bench_qkv(args.steps, 1)
+            continue
+        if name in ("partials_merge_t1", "partials_merge_t4"):
+            bench_merge(args.steps, 1, n_tok=int(name[-1]))
+            continue
         if name == "copy":  # calibration: a plain 256 MiB device copy
             x = torch.ones(256 << 20, dtype=torch.uint8, device="cuda")
             y = torch.empty_like(x)
