@@ -101,7 +101,8 @@ def test_workspace_too_small_is_reported():
 
 
 def test_baseline_work_counts():
-    # BASELINE.md section 2 figures
+    # the work of each benchmark shape: K/V bytes of a decode call, flops of a
+    # prefill (4 hd per visible query-key pair, causal pairs with the diagonal)
     assert wl.kv_bytes(wl.C1) == 16_793_600
     assert wl.kv_bytes(wl.C2) == 16_809_984
     assert wl.kv_bytes(wl.C3_FULL) == 67_141_632
