@@ -692,7 +692,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
 }
 
 // Sliding-window prefill over consecutive token blocks (head dim 64, 8
-// heads per kv head, windows up to 130 keys).  One 8-wave workgroup per CU
+// heads per kv head, windows up to 130 keys, linear or ring caches).  One
+// 8-wave workgroup per CU
 // takes `spw` consecutive 64-token blocks of one kv head.  Keys sit in LDS
 // as a ring of 32-key chunks (slot = chunk mod NCH): consecutive blocks
 // share all but their last two chunks, so a block brings in two new chunks
@@ -703,7 +704,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
 // has no waits or barriers; one barrier per block hands the ring over.
 // The chunk step is the one of prefill_kernel (same pipeline, same lazy
 // softmax), with ring addresses in place of tile buffers.
-template <int NCH>
+template <int NCH, bool RING>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_slide_kernel(
     PrefillParams p, int n_parts, int spw) {
     constexpr int HD = 64, RT = 2, NW = 8, KS = HD / 16, DT = HD / 32, PPR = HD / 8, HPK = 8;
@@ -750,10 +751,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int n_steps = (p.T + TBK - 1) / TBK;
     const int j0 = part * spw, j1 = min(j0 + spw, n_steps);
     if (j0 >= j1) return;
-    const int64_t row0 = p.seq_off ? p.seq_off[s] : (int64_t)s * p.kv_len;
+    const int64_t row0 = p.seq_off ? p.seq_off[s] : (int64_t)s * (RING ? p.ring_cap : p.kv_len);
     const int qoff0 = len - p.T;  // position of token 0
     const uint32_t stride_b = (uint32_t)p.row_stride * 2;
-    const uint32_t nrec = (uint32_t)len * stride_b;
+    // (ring caches: key j sits in row j % ring_cap)
+    const uint32_t nrec = (uint32_t)(RING ? p.ring_cap : len) * stride_b;
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(p.k + row0 * p.row_stride + (size_t)kvh * HD), (short)0, (int)nrec, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
@@ -775,7 +777,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const bool is_v = wave >= 4;
         const int q = 64 * (wave & 3) + lane, key = q / PPR, phys = q % PPR;
         const int piece = is_v ? phys ^ ((key & 3) << 1) : phys ^ (key & 7);
-        const uint32_t off = (uint32_t)(32 * c + key) * stride_b + 16 * piece;
+        const int krow = RING ? (32 * c + key) % p.ring_cap : 32 * c + key;
+        const uint32_t off = (uint32_t)krow * stride_b + 16 * piece;
         char* const dst = (is_v ? vring : kring) + slot(c) * CHB + 1024 * (wave & 3);
         if (tracked) lds_dma16(is_v ? rv : rk, off, dst);
         else lds_dma16_untracked(is_v ? rv : rk, off, dst);
@@ -1205,9 +1208,9 @@ static int prefill_cus() {
 }
 
 // the sliding-window kernel's shapes: head dim 64, 8 heads per kv head,
-// linear caches, whole-prompt launches, a window the ring holds
+// whole-prompt launches, a window its chunk ring holds
 static bool slide_fits(const PrefillParams& p) {
-    return !kNoSlide && p.hd == 64 && p.hpk == 8 && !p.ring_cap && !p.state && p.window > 0 &&
+    return !kNoSlide && p.hd == 64 && p.hpk == 8 && !p.state && p.window > 0 &&
            (126 + p.window) / 32 + 2 <= kSlideChunks;
 }
 
@@ -1219,7 +1222,12 @@ static hipError_t launch_slide(const PrefillParams& p, hipStream_t st) {
     const long long nblk = (long long)n_parts * p.n_kv * p.n_seq;
     if (nblk > 0x7fffffff) return hipErrorNotSupported;
     ProfScope ps(kProfPrefill, st);
-    hipLaunchKernelGGL((prefill_slide_kernel<kSlideChunks>), dim3((unsigned)nblk), dim3(512), 0, st, p, n_parts, spw);
+    if (p.ring_cap)
+        hipLaunchKernelGGL((prefill_slide_kernel<kSlideChunks, true>), dim3((unsigned)nblk), dim3(512), 0, st, p, n_parts,
+                           spw);
+    else
+        hipLaunchKernelGGL((prefill_slide_kernel<kSlideChunks, false>), dim3((unsigned)nblk), dim3(512), 0, st, p,
+                           n_parts, spw);
     return hipGetLastError();
 }
 
