@@ -152,3 +152,35 @@ def test_slide_window_logits_far_below_zero():
     inp.q.copy_(qv.half().expand_as(inp.q))
     print("[case] slide window logit -120", flush=True)
     assert_close(as_f64(gpu_run(inp)), as_f64(oracle_run(inp)), what="slide window logit -120")
+
+
+def test_slide_window_ring_ragged_sequences():
+    # two sequences, each with its own ring of `cap` rows (key j of sequence
+    # s in row s*cap + j % cap), ragged lengths, window 128
+    from oracle import oracle as orc
+    from pelica_amd import attn
+    from tests.gpu_util import to_np_f16
+
+    T, W = 300, 128
+    cfg = wl.AttnConfig("pringr", "prefill", 64, 8, 64, 1300, q_tokens=T, window=W, sinks=True, n_seq=2,
+                        ragged=(700, 1300), seed=91)
+    inp = wl.make_inputs(cfg, "cuda")
+    cap = W + T
+    lens = inp.seq_len.cpu().tolist()
+    offs = inp.seq_off.cpu().tolist()
+    kr = torch.zeros(2 * cap, 8, 64, dtype=torch.float16, device="cuda")
+    vr = torch.zeros_like(kr)
+    for s_i, (n, off) in enumerate(zip(lens, offs)):
+        j = torch.arange(n - cap, n, device="cuda")
+        kr[s_i * cap + j % cap] = inp.k[off + j]
+        vr[s_i * cap + j % cap] = inp.v[off + j]
+    ring_off = torch.tensor([0, cap], dtype=torch.int64, device="cuda")
+    print("[case] slide window ring ragged", flush=True)
+    got = attn.prefill(inp.q, kr, vr, n_kv=8, kv_len=inp.kv_len, sinks=inp.sinks, window=W, ring_cap=cap,
+                       seq_kv_len=inp.seq_len, seq_kv_offset=ring_off)
+    torch.cuda.synchronize()
+    ref = orc.attention(inp.q.cpu().numpy().view(np.uint16), to_np_f16(kr), to_np_f16(vr), n_kv=8,
+                        kv_len=inp.kv_len, seq_kv_len=inp.seq_len.cpu().numpy(),
+                        seq_kv_offset=np.array([0, cap], dtype=np.int64), sinks=inp.sinks.cpu().numpy(), window=W,
+                        ring_cap=cap)
+    assert_close(as_f64(got), as_f64(ref), what="slide ring ragged")
