@@ -37,6 +37,23 @@ typedef _Float16 half2 __attribute__((ext_vector_type(2)));
 
 // word 3 of a gfx9 buffer resource: 32-bit data format, raw addressing
 constexpr int kBufferFlags = 0x00020000;
+#ifndef PELICA_SLIDE_LOAD_AUX
+#define PELICA_SLIDE_LOAD_AUX 0
+#endif
+#ifndef PELICA_SLIDE_STORE_AUX
+#define PELICA_SLIDE_STORE_AUX 2
+#endif
+#ifndef PELICA_PRE_STORE_AUX
+#define PELICA_PRE_STORE_AUX 2
+#endif
+// Cache policy of the query loads and output stores (each byte touched
+// once).  Output stores go nt (streaming), so they do not displace the K/V
+// the kv head's workgroups share in L2: the sliding-window kernel's
+// window-128 prompt 26.5-26.6 -> 23.5-24.8 us (nt query loads as well:
+// 26.9-28.1; nt query loads alone: 31.5-31.9), the full causal prompt
+// 151.9-152.3 -> 150.8-151.4 us.
+constexpr int kSlideLoadAux = PELICA_SLIDE_LOAD_AUX, kSlideStoreAux = PELICA_SLIDE_STORE_AUX;
+constexpr int kPreStoreAux = PELICA_PRE_STORE_AUX;
 
 __device__ __forceinline__ float16v mfma32(const half8& a, const half8& b, const float16v& c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -632,7 +649,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
             const uint32_t off = r < TB * p.hpk ? (uint32_t)(r / p.hpk) * otok_b +
                                                       (uint32_t)((kvh * p.hpk + r % p.hpk) * HD + 8 * pc) * 2
                                                 : 0xFFFFFF00u;  // (rows past the block's token count)
-            __builtin_amdgcn_raw_buffer_store_b128(val[k], ro, off, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(val[k], ro, off, 0, kPreStoreAux);
         }
     } else {
     // O^T lane layout: dim 32 dt + 8 (i / 4) + 4 h2 + i % 4 of row c32
@@ -794,7 +811,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const int row = HPK * i + hr;
             const uint32_t off = (uint32_t)(HPK * wave + i) * qtok_b + (uint32_t)((kvh * HPK + hr) * HD) * 2 +
                                  16 * (phys ^ (row & 7));
-            lds_dma16_untracked(rq, off, stage + 1024 * i);
+            lds_dma16_untracked<kSlideLoadAux == 2>(rq, off, stage + 1024 * i);
         }
     };
 
@@ -811,7 +828,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const uint32_t qoff = (uint32_t)(r / HPK) * qtok_b + (uint32_t)((kvh * HPK + r % HPK) * HD + 8 * h2) * 2;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks)
-                qb[rt][ks] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + 32 * ks, 0, 0));
+                qb[rt][ks] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + 32 * ks, 0, kSlideLoadAux));
         }
     }
     float sk[RT];
@@ -867,7 +884,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int k = 0; k < NST; ++k) {
             const int r = wave * RT * 32 + k * RPI + lane / PPR;  // token r / HPK of the block, head r % HPK
             const uint32_t off = (uint32_t)(r / HPK) * otok_b + (uint32_t)((kvh * HPK + r % HPK) * HD + 8 * pc) * 2;
-            __builtin_amdgcn_raw_buffer_store_b128(val[k], ro, off, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(val[k], ro, off, 0, kSlideStoreAux);
         }
     };
 
