@@ -32,7 +32,7 @@ F16_PEAK_TFLOPS = 2500.0    # MI355X dense f16 MFMA
 # plain copy of known size moves, while WRITE_SIZE reads them exactly
 # (profiles/hbm_traffic_counters.md).
 HBM_TRAFFIC_C3 = 69_744_435   # 32902.9 KiB fetched (x2) + 2304.0 KiB written per split launch
-HBM_TRAFFIC_C4 = 77_112_115   # 21268.4 KiB fetched (x2) + 32768 KiB written per prefill launch
+HBM_TRAFFIC_C4 = 75_917_312   # 20685.1 KiB fetched (x2) + 32768 KiB written per prefill launch
 
 
 def parse():
