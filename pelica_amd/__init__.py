@@ -11,6 +11,7 @@ from .attn import (  # noqa: F401
     Rope,
     Shape,
     decode,
+    decode_noalloc,
     decode_partials,
     default_scale,
     library_path,
@@ -25,6 +26,7 @@ from .attn import (  # noqa: F401
     prof_enable,
     prof_read,
     qkv_rope_cache,
+    reload_tuning,
     workspace_bytes,
 )
 
@@ -34,6 +36,7 @@ __all__ = [
     "Rope",
     "Shape",
     "decode",
+    "decode_noalloc",
     "decode_partials",
     "default_scale",
     "library_path",
@@ -48,5 +51,6 @@ __all__ = [
     "prof_enable",
     "prof_read",
     "qkv_rope_cache",
+    "reload_tuning",
     "workspace_bytes",
 ]

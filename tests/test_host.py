@@ -171,3 +171,16 @@ def test_noalloc_scratch_size_matches_header():
     text = open(os.path.join(ROOT, "include", "pelica_attn.h")).read()
     m = re.search(r"#define PELICA_ATTN_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", text)
     assert m and int(m.group(1)) << int(m.group(2)) == attn.NOALLOC_SCRATCH_BYTES
+
+
+def test_package_exports_every_public_binding():
+    """Every public function of the binding module is re-exported by the package."""
+    import inspect
+
+    import pelica_amd
+
+    public = {n for n, f in inspect.getmembers(attn, inspect.isfunction)
+              if not n.startswith("_") and f.__module__ == attn.__name__}
+    assert public <= set(pelica_amd.__all__), sorted(public - set(pelica_amd.__all__))
+    for n in pelica_amd.__all__:
+        assert getattr(pelica_amd, n) is getattr(attn, n)
