@@ -197,7 +197,8 @@ int pelica_attn_partials_merge(int32_t n_head, int32_t hd, int32_t n_parts,
  * rows of a draft-verify pass): slot c of token t, head h at
  * parts[((c*n_tokens + t)*n_head + h)*(hd+2)], output out[t][n_head][hd]
  * (so the slots that pelica_attn_decode_partials writes for a whole pass are
- * one slot c here).  Each slot's weight is computed once per (token, head).
+ * one slot c here).  Every thread loads its slots in one round trip and
+ * computes their weights itself (no staging barrier).
  * Replaces ATTN_M over its (n_head, TMAX) grid (src/oss_batch.rs:395-425)
  * and merge_dec_fast (src/moe_kernels.rs:750-808). */
 int pelica_attn_partials_merge_batch(int32_t n_tokens, int32_t n_head, int32_t hd, int32_t n_parts,
