@@ -9,7 +9,15 @@
  * thread's last error is available from pelica_attn_last_error().
  *
  * Layouts (f16 = IEEE binary16 stored as uint16_t):
- *   q, out   [n_seq][q_tokens][n_head][hd]
+ *   q, out   token i = s * q_tokens + t holds its n_head * hd values (head
+ *            h at h * hd) starting at element i * q_token_stride (q) or
+ *            i * out_token_stride (out); stride 0 = n_head * hd, i.e.
+ *            [n_seq][q_tokens][n_head][hd].  A nonzero stride lets the
+ *            queries stay in place in the engine's fused [q | k | v] rows
+ *            and the output go straight into a wider activation row, as
+ *            the reference's kernels read and write them (q stride arg 9,
+ *            out stride arg 10: src/oss_batch.rs:172-176,267-270,
+ *            src/oss_prefill.rs:400-402, set at src/oss.rs:680,690,693,739).
  *   k, v     cache rows of n_kv*hd values, row r at k + r*kv_row_stride;
  *            key position j of sequence s lives in row
  *            seq_kv_offset[s] + (ring_cap ? j % ring_cap : j)
@@ -35,7 +43,7 @@
 extern "C" {
 #endif
 
-#define PELICA_ATTN_VERSION 1
+#define PELICA_ATTN_VERSION 2
 
 /* status codes */
 #define PELICA_ATTN_OK 0
@@ -65,6 +73,10 @@ typedef struct PelicaAttnDesc {
                           (src/oss_batch.rs:205, src/oss.rs:570-572) */
     float scale;       /* logit scale; 0 = 1/sqrt(hd) (src/moe.rs:1263) */
     uint32_t flags;    /* 0, or PELICA_ATTN_FLAG_SPLIT_ONLY (pelica_attn_decode only) */
+    int64_t q_token_stride;   /* elements between consecutive query tokens; 0 = n_head * hd.
+                                 A multiple of 4 (f32 queries) or 8 (f16), >= n_head * hd */
+    int64_t out_token_stride; /* elements between consecutive output tokens; 0 = n_head * hd.
+                                 A multiple of 4 (f32 output) or 8 (f16), >= n_head * hd */
 } PelicaAttnDesc;
 
 /* Measurement flag (no counterpart in the reference): pelica_attn_decode
@@ -84,7 +96,7 @@ const char* pelica_attn_last_error(void);
  * planner's PELICA_ATTN_* tuning variables are read from the environment
  * once, at the first call that plans a pass; this re-reads them.  Plans and
  * workspace sizes may change with it: size workspaces again afterwards.
- * Not safe while another thread plans a call. */
+ * Calls planned concurrently with it use either the old or the new values. */
 int pelica_attn_reload_tuning(void);
 
 /* Bytes of device workspace pelica_attn_decode needs for this descriptor
@@ -144,6 +156,23 @@ int pelica_attn_decode_partials(const PelicaAttnDesc* desc, const float* q, cons
                                 const uint16_t* v, float* parts, void* workspace,
                                 size_t workspace_bytes, void* stream);
 
+/* Decode partials over one range of key positions [key_begin, key_end)
+ * whose cache rows start at k_rows / v_rows (row 0 = position key_begin),
+ * e.g. the rows past `res` that the reference keeps in host memory (its
+ * "far" buffers).  Same slots and workspace as pelica_attn_decode_partials
+ * (rows that see no key of the range get M = -3e38, L = 0, O = 0); one
+ * sequence (n_seq 1, no seq_kv_len), linear cache (ring_cap 0);
+ * 0 <= key_begin < key_end <= kv_len.  The reference's attn_s reads its
+ * keys below res from VRAM and the rest from the far buffers in one
+ * dispatch (src/oss_batch.rs:253-393, args 3 and 10; src/oss.rs:685-693);
+ * here that pass is two of these calls, [0, res) over the VRAM rows and
+ * [res, kv_len) over the far rows, whose slots pelica_attn_partials_merge_batch
+ * combines with the sinks (ATTN_M, src/oss_batch.rs:395-425). */
+int pelica_attn_decode_partials_range(const PelicaAttnDesc* desc, const float* q, const uint16_t* k_rows,
+                                      const uint16_t* v_rows, int32_t key_begin, int32_t key_end,
+                                      float* parts, void* workspace, size_t workspace_bytes,
+                                      void* stream);
+
 /* MLA (latent) attention: one kv head whose keys and values are the same
  * latent cache rows, hd = 512 f16 per position (row stride kv_row_stride,
  * 0 = 512); n_kv must be 1; q: the absorbed f32 queries
@@ -164,6 +193,14 @@ int pelica_attn_mla(const PelicaAttnDesc* desc, const float* q, const uint16_t* 
 int pelica_attn_prefill(const PelicaAttnDesc* desc, const uint16_t* q, const uint16_t* k,
                         const uint16_t* v, const float* sinks, uint16_t* out, void* stream);
 
+/* The same prompt attention with f32 queries and f32 output, the layout
+ * the reference's attn_p reads and writes (q f32 rows at stride qkv_rows,
+ * xo f32 at stride attw: src/oss_prefill.rs:391-526, src/oss.rs:734-741).
+ * The queries are rounded to f16 for the QK^T products (as the f16 cache
+ * rows are); softmax and accumulation stay f32. */
+int pelica_attn_prefill_f32(const PelicaAttnDesc* desc, const float* q, const uint16_t* k,
+                            const uint16_t* v, const float* sinks, float* out, void* stream);
+
 /* Prompt attention over one round of keys: the cache rows of key positions
  * [key_begin, key_end) (k_rows / v_rows row 0 = position key_begin, e.g. a
  * staging copy of rows that live past HBM) folded into a running state per
@@ -180,6 +217,12 @@ int pelica_attn_prefill_round(const PelicaAttnDesc* desc, const uint16_t* q, con
                               const uint16_t* v_rows, int32_t key_begin, int32_t key_end,
                               const float* sinks, float* state, int32_t first, uint16_t* out,
                               void* stream);
+
+/* prefill_round with f32 queries and f32 out (see pelica_attn_prefill_f32). */
+int pelica_attn_prefill_round_f32(const PelicaAttnDesc* desc, const float* q, const uint16_t* k_rows,
+                                  const uint16_t* v_rows, int32_t key_begin, int32_t key_end,
+                                  const float* sinks, float* state, int32_t first, float* out,
+                                  void* stream);
 
 /* Combine n_parts partial slots of one decode token (parts[(c*n_head+h)*(hd+2)],
  * natural-log max) in slot order, with optional sinks, into out[n_head][hd].

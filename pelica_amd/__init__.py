@@ -13,6 +13,7 @@ from .attn import (  # noqa: F401
     decode,
     decode_noalloc,
     decode_partials,
+    decode_partials_range,
     default_scale,
     library_path,
     load_library,
@@ -27,6 +28,7 @@ from .attn import (  # noqa: F401
     prof_read,
     qkv_rope_cache,
     reload_tuning,
+    token_stride,
     workspace_bytes,
 )
 
@@ -38,6 +40,7 @@ __all__ = [
     "decode",
     "decode_noalloc",
     "decode_partials",
+    "decode_partials_range",
     "default_scale",
     "library_path",
     "load_library",
@@ -52,5 +55,6 @@ __all__ = [
     "prof_read",
     "qkv_rope_cache",
     "reload_tuning",
+    "token_stride",
     "workspace_bytes",
 ]

@@ -38,10 +38,13 @@ EXPORTS = (
     "pelica_attn_decode",
     "pelica_attn_decode_noalloc",
     "pelica_attn_decode_partials",
+    "pelica_attn_decode_partials_range",
     "pelica_attn_mla_workspace_bytes",
     "pelica_attn_mla",
     "pelica_attn_prefill",
+    "pelica_attn_prefill_f32",
     "pelica_attn_prefill_round",
+    "pelica_attn_prefill_round_f32",
     "pelica_attn_partials_merge",
     "pelica_attn_partials_merge_batch",
     "pelica_attn_qkv_rope_cache",
@@ -116,6 +119,8 @@ class AttnDesc(ctypes.Structure):
         ("ring_cap", ctypes.c_int32),
         ("scale", ctypes.c_float),
         ("flags", ctypes.c_uint32),
+        ("q_token_stride", ctypes.c_int64),
+        ("out_token_stride", ctypes.c_int64),
     ]
 
 
@@ -157,14 +162,20 @@ def load_library() -> ctypes.CDLL:
     lib.pelica_attn_decode_noalloc.argtypes = [dp, vp, vp, vp, vp, vp, vp]
     lib.pelica_attn_decode_partials.restype = ctypes.c_int
     lib.pelica_attn_decode_partials.argtypes = [dp, vp, vp, vp, vp, vp, sz, vp]
+    lib.pelica_attn_decode_partials_range.restype = ctypes.c_int
+    lib.pelica_attn_decode_partials_range.argtypes = [dp, vp, vp, vp, i32, i32, vp, vp, sz, vp]
     lib.pelica_attn_prefill.restype = ctypes.c_int
     lib.pelica_attn_prefill.argtypes = [dp, vp, vp, vp, vp, vp, vp]
+    lib.pelica_attn_prefill_f32.restype = ctypes.c_int
+    lib.pelica_attn_prefill_f32.argtypes = [dp, vp, vp, vp, vp, vp, vp]
     lib.pelica_attn_mla_workspace_bytes.restype = sz
     lib.pelica_attn_mla_workspace_bytes.argtypes = [dp]
     lib.pelica_attn_mla.restype = ctypes.c_int
     lib.pelica_attn_mla.argtypes = [dp, vp, vp, vp, vp, sz, vp]
     lib.pelica_attn_prefill_round.restype = ctypes.c_int
     lib.pelica_attn_prefill_round.argtypes = [dp, vp, vp, vp, i32, i32, vp, vp, i32, vp, vp]
+    lib.pelica_attn_prefill_round_f32.restype = ctypes.c_int
+    lib.pelica_attn_prefill_round_f32.argtypes = [dp, vp, vp, vp, i32, i32, vp, vp, i32, vp, vp]
     lib.pelica_attn_qkv_rope_cache.restype = ctypes.c_int
     lib.pelica_attn_qkv_rope_cache.argtypes = [dp, ctypes.POINTER(Rope), vp, vp, vp, ctypes.c_int64, vp, vp,
                                                ctypes.c_float, vp, vp, vp]
@@ -200,7 +211,8 @@ def _stream_ptr(stream) -> Optional[int]:
 
 def make_desc(n_head: int, n_kv: int, hd: int, *, n_seq: int = 1, q_tokens: int = 1, kv_len: int,
               seq_kv_len=None, seq_kv_offset=None, kv_row_stride: int = 0, window: int = 0,
-              ring_cap: int = 0, scale: Optional[float] = None, flags: int = 0) -> AttnDesc:
+              ring_cap: int = 0, scale: Optional[float] = None, flags: int = 0, q_token_stride: int = 0,
+              out_token_stride: int = 0) -> AttnDesc:
     d = AttnDesc()
     d.n_head, d.n_kv, d.hd = n_head, n_kv, hd
     d.n_seq, d.q_tokens, d.kv_len = n_seq, q_tokens, kv_len
@@ -210,7 +222,24 @@ def make_desc(n_head: int, n_kv: int, hd: int, *, n_seq: int = 1, q_tokens: int 
     d.window, d.ring_cap = window, ring_cap
     d.scale = 0.0 if scale is None else float(scale)
     d.flags = flags
+    d.q_token_stride, d.out_token_stride = q_token_stride, out_token_stride
     return d
+
+
+def token_stride(t) -> int:
+    """The descriptor's token stride for a [n_seq, T, n_head, hd] tensor:
+    0 when it is contiguous, else the elements between consecutive tokens
+    (s * T + t) of a view whose heads are contiguous — e.g. the queries left
+    in place in fused [q | k | v] rows.  Raises for other layouts."""
+    if t.is_contiguous():
+        return 0
+    n_seq, T, n_head, hd = t.shape
+    if t.stride(3) != 1 or (n_head > 1 and t.stride(2) != hd):
+        raise AttnError(EINVAL, f"token rows need contiguous heads, got strides {tuple(t.stride())}")
+    st = t.stride(1) if T > 1 else t.stride(0)
+    if n_seq > 1 and T > 1 and t.stride(0) != T * st:
+        raise AttnError(EINVAL, f"tokens of all sequences need one stride, got strides {tuple(t.stride())}")
+    return st
 
 
 def _validate_lens(seq_kv_len, seq_kv_offset):
@@ -232,10 +261,11 @@ def workspace_bytes(desc: AttnDesc) -> int:
 
 
 def new_workspace(desc: AttnDesc, device="cuda"):
-    """A zero-filled workspace for decode calls with this descriptor."""
+    """A workspace for decode calls with this descriptor (uninitialised:
+    the calls need no particular contents)."""
     import torch
 
-    return torch.zeros(max(workspace_bytes(desc), 16), dtype=torch.uint8, device=device)
+    return torch.empty(max(workspace_bytes(desc), 16), dtype=torch.uint8, device=device)
 
 
 def decode(q, k, v, *, n_kv: int, kv_len: int, sinks=None, window: int = 0, ring_cap: int = 0,
@@ -247,23 +277,26 @@ def decode(q, k, v, *, n_kv: int, kv_len: int, sinks=None, window: int = 0, ring
     (PELICA_ATTN_FLAG_SPLIT_ONLY); the result is then not written."""
     import torch
 
-    assert q.dtype == torch.float32 and q.dim() == 4 and q.is_contiguous() and q.is_cuda
+    assert q.dtype == torch.float32 and q.dim() == 4 and q.is_cuda
     assert k.dtype == torch.float16 and v.dtype == torch.float16 and k.is_contiguous() and v.is_contiguous()
     _validate_lens(seq_kv_len, seq_kv_offset)
     n_seq, T, n_head, hd = q.shape
+    if out is None:
+        out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    assert out.dtype == torch.float32 and out.shape == q.shape
     desc = make_desc(n_head, n_kv, hd, n_seq=n_seq, q_tokens=T, kv_len=kv_len, seq_kv_len=seq_kv_len,
                      seq_kv_offset=seq_kv_offset, kv_row_stride=kv_row_stride, window=window,
-                     ring_cap=ring_cap, scale=scale, flags=FLAG_SPLIT_ONLY if split_only else 0)
+                     ring_cap=ring_cap, scale=scale, flags=FLAG_SPLIT_ONLY if split_only else 0,
+                     q_token_stride=token_stride(q), out_token_stride=token_stride(out))
     lib = load_library()
     need = lib.pelica_attn_workspace_bytes(ctypes.byref(desc))
     if need == 0:
         msg = lib.pelica_attn_last_error().decode(errors="replace")
         if msg:
             raise AttnError(EINVAL, msg)
-    if out is None:
-        out = torch.empty_like(q)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
-        workspace = torch.zeros(need, dtype=torch.uint8, device=q.device)
+        # (the contents need no initialisation)
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     if sinks is not None:
         assert sinks.dtype == torch.float32 and sinks.is_cuda and sinks.numel() == n_head
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
@@ -283,15 +316,16 @@ def decode_noalloc(q, k, v, *, n_kv: int, kv_len: int, sinks=None, window: int =
     library's per-device static scratch (calls on one GPU must not overlap)."""
     import torch
 
-    assert q.dtype == torch.float32 and q.dim() == 4 and q.is_contiguous() and q.is_cuda
+    assert q.dtype == torch.float32 and q.dim() == 4 and q.is_cuda
     assert k.dtype == torch.float16 and v.dtype == torch.float16 and k.is_contiguous() and v.is_contiguous()
     _validate_lens(seq_kv_len, seq_kv_offset)
     n_seq, T, n_head, hd = q.shape
+    if out is None:
+        out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
     desc = make_desc(n_head, n_kv, hd, n_seq=n_seq, q_tokens=T, kv_len=kv_len, seq_kv_len=seq_kv_len,
                      seq_kv_offset=seq_kv_offset, kv_row_stride=kv_row_stride, window=window,
-                     ring_cap=ring_cap, scale=scale)
-    if out is None:
-        out = torch.empty_like(q)
+                     ring_cap=ring_cap, scale=scale, q_token_stride=token_stride(q),
+                     out_token_stride=token_stride(out))
     if sinks is not None:
         assert sinks.dtype == torch.float32 and sinks.is_cuda and sinks.numel() == n_head
     _check(load_library().pelica_attn_decode_noalloc(ctypes.byref(desc), _ptr(q), _ptr(k), _ptr(v), _ptr(sinks),
@@ -307,26 +341,59 @@ def decode_partials(q, k, v, *, n_kv: int, kv_len: int, window: int = 0, ring_ca
     (they join in ``partials_merge`` with the CPU tier's slots)."""
     import torch
 
-    assert q.dtype == torch.float32 and q.dim() == 4 and q.is_contiguous() and q.is_cuda
+    assert q.dtype == torch.float32 and q.dim() == 4 and q.is_cuda
     assert k.dtype == torch.float16 and v.dtype == torch.float16 and k.is_contiguous() and v.is_contiguous()
     _validate_lens(seq_kv_len, seq_kv_offset)
     n_seq, T, n_head, hd = q.shape
     desc = make_desc(n_head, n_kv, hd, n_seq=n_seq, q_tokens=T, kv_len=kv_len, seq_kv_len=seq_kv_len,
                      seq_kv_offset=seq_kv_offset, kv_row_stride=kv_row_stride, window=window,
-                     ring_cap=ring_cap, scale=scale)
+                     ring_cap=ring_cap, scale=scale, q_token_stride=token_stride(q))
     lib = load_library()
+    if parts is None:
+        parts = torch.empty(n_seq, T, n_head, hd + 2, dtype=torch.float32, device=q.device)
+    workspace, ws_bytes = _decode_workspace(lib, desc, workspace, q.device)
+    _check(lib.pelica_attn_decode_partials(ctypes.byref(desc), _ptr(q), _ptr(k), _ptr(v), _ptr(parts),
+                                           _ptr(workspace), ws_bytes, _stream_ptr(stream)))
+    return parts
+
+
+def _decode_workspace(lib, desc, workspace, device):
+    """(workspace, bytes): the caller's, or a new one when it is missing or
+    too small for this descriptor's plan."""
+    import torch
+
     need = lib.pelica_attn_workspace_bytes(ctypes.byref(desc))
     if need == 0:
         msg = lib.pelica_attn_last_error().decode(errors="replace")
         if msg:
             raise AttnError(EINVAL, msg)
-    if parts is None:
-        parts = torch.empty(n_seq, T, n_head, hd + 2, dtype=torch.float32, device=q.device)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
-        workspace = torch.zeros(need, dtype=torch.uint8, device=q.device)
-    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
-    _check(lib.pelica_attn_decode_partials(ctypes.byref(desc), _ptr(q), _ptr(k), _ptr(v), _ptr(parts),
-                                           _ptr(workspace), ws_bytes, _stream_ptr(stream)))
+        workspace = torch.empty(need, dtype=torch.uint8, device=device)
+    return workspace, 0 if workspace is None else workspace.numel() * workspace.element_size()
+
+
+def decode_partials_range(q, k_rows, v_rows, *, n_kv: int, kv_len: int, key_begin: int, key_end: int,
+                          window: int = 0, scale: Optional[float] = None, kv_row_stride: int = 0, parts=None,
+                          workspace=None, stream=None):
+    """Partials over key positions [key_begin, key_end) whose cache rows
+    start at k_rows / v_rows (row 0 = position key_begin), one sequence:
+    f32 [1, q_tokens, n_head, hd + 2] slots like ``decode_partials``.  Two
+    such calls (VRAM rows, far rows) and ``partials_merge_batch`` are the
+    reference's attn_s over resident and far keys."""
+    import torch
+
+    assert q.dtype == torch.float32 and q.dim() == 4 and q.is_cuda and q.shape[0] == 1
+    assert k_rows.dtype == v_rows.dtype == torch.float16 and k_rows.is_contiguous() and v_rows.is_contiguous()
+    n_seq, T, n_head, hd = q.shape
+    desc = make_desc(n_head, n_kv, hd, n_seq=1, q_tokens=T, kv_len=kv_len, kv_row_stride=kv_row_stride,
+                     window=window, scale=scale, q_token_stride=token_stride(q))
+    lib = load_library()
+    if parts is None:
+        parts = torch.empty(1, T, n_head, hd + 2, dtype=torch.float32, device=q.device)
+    workspace, ws_bytes = _decode_workspace(lib, desc, workspace, q.device)
+    _check(lib.pelica_attn_decode_partials_range(ctypes.byref(desc), _ptr(q), _ptr(k_rows), _ptr(v_rows),
+                                                 key_begin, key_end, _ptr(parts), _ptr(workspace), ws_bytes,
+                                                 _stream_ptr(stream)))
     return parts
 
 
@@ -365,24 +432,29 @@ def qkv_rope_cache(q, k, v, k_cache, v_cache, *, n_kv: int, kv_len: int, table=N
 def prefill(q, k, v, *, n_kv: int, kv_len: Optional[int] = None, sinks=None, window: int = 0,
             ring_cap: int = 0, scale: Optional[float] = None, seq_kv_len=None, seq_kv_offset=None,
             kv_row_stride: int = 0, out=None, stream=None):
-    """Prompt attention.  q: f16 [n_seq, T, n_head, hd]; k, v: f16 cache rows;
-    kv_len defaults to T (a prompt that starts the cache).  Returns f16."""
+    """Prompt attention.  q: f16 (pelica_attn_prefill) or f32
+    (pelica_attn_prefill_f32) [n_seq, T, n_head, hd], contiguous or token
+    rows of a wider buffer; k, v: f16 cache rows; kv_len defaults to T (a
+    prompt that starts the cache).  Returns q's dtype (or fills ``out``, which
+    may be a strided view too)."""
     import torch
 
-    assert q.dtype == torch.float16 and q.dim() == 4 and q.is_contiguous() and q.is_cuda
+    assert q.dtype in (torch.float16, torch.float32) and q.dim() == 4 and q.is_cuda
     assert k.dtype == torch.float16 and v.dtype == torch.float16 and k.is_contiguous() and v.is_contiguous()
     _validate_lens(seq_kv_len, seq_kv_offset)
     n_seq, T, n_head, hd = q.shape
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    assert out.dtype == q.dtype and out.shape == q.shape
     desc = make_desc(n_head, n_kv, hd, n_seq=n_seq, q_tokens=T, kv_len=T if kv_len is None else kv_len,
                      seq_kv_len=seq_kv_len, seq_kv_offset=seq_kv_offset, kv_row_stride=kv_row_stride,
-                     window=window, ring_cap=ring_cap, scale=scale)
-    if out is None:
-        out = torch.empty_like(q)
+                     window=window, ring_cap=ring_cap, scale=scale, q_token_stride=token_stride(q),
+                     out_token_stride=token_stride(out))
     if sinks is not None:
         assert sinks.dtype == torch.float32 and sinks.is_cuda and sinks.numel() == n_head
     lib = load_library()
-    _check(lib.pelica_attn_prefill(ctypes.byref(desc), _ptr(q), _ptr(k), _ptr(v), _ptr(sinks), _ptr(out),
-                                   _stream_ptr(stream)))
+    fn = lib.pelica_attn_prefill if q.dtype == torch.float16 else lib.pelica_attn_prefill_f32
+    _check(fn(ctypes.byref(desc), _ptr(q), _ptr(k), _ptr(v), _ptr(sinks), _ptr(out), _stream_ptr(stream)))
     return out
 
 
@@ -393,20 +465,21 @@ def mla(q, latent, *, kv_len: int, scale: Optional[float] = None, seq_kv_len=Non
     Returns f32 like q."""
     import torch
 
-    assert q.dtype == torch.float32 and q.dim() == 4 and q.is_contiguous() and q.is_cuda and q.shape[-1] == 512
+    assert q.dtype == torch.float32 and q.dim() == 4 and q.is_cuda and q.shape[-1] == 512
     assert latent.dtype == torch.float16 and latent.is_contiguous()
     _validate_lens(seq_kv_len, seq_kv_offset)
     n_seq, T, n_head, hd = q.shape
+    if out is None:
+        out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
     desc = make_desc(n_head, 1, hd, n_seq=n_seq, q_tokens=T, kv_len=kv_len, seq_kv_len=seq_kv_len,
-                     seq_kv_offset=seq_kv_offset, kv_row_stride=kv_row_stride, scale=scale)
+                     seq_kv_offset=seq_kv_offset, kv_row_stride=kv_row_stride, scale=scale,
+                     q_token_stride=token_stride(q), out_token_stride=token_stride(out))
     lib = load_library()
     need = lib.pelica_attn_mla_workspace_bytes(ctypes.byref(desc))
     if need == 0:
         msg = lib.pelica_attn_last_error().decode(errors="replace")
         if msg:
             raise AttnError(EINVAL, msg)
-    if out is None:
-        out = torch.empty_like(q)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
@@ -420,20 +493,23 @@ def prefill_round(q, k_rows, v_rows, state, *, n_kv: int, kv_len: int, key_begin
                   kv_row_stride: int = 0, out=None, stream=None):
     """Prompt attention over one round of keys [key_begin, key_end) (rows of
     those positions in k_rows / v_rows), folded into ``state`` (f32 [1, T,
-    n_head, hd + 2]: M natural-log, L, O); ``out`` (f16 like q) gets the
-    output so far when given.  Returns out (or None)."""
+    n_head, hd + 2]: M natural-log, L, O); ``out`` (q's dtype: f16, or f32
+    through pelica_attn_prefill_round_f32) gets the output so far when
+    given.  Returns out (or None)."""
     import torch
 
-    assert q.dtype == torch.float16 and q.dim() == 4 and q.is_contiguous() and q.is_cuda
+    assert q.dtype in (torch.float16, torch.float32) and q.dim() == 4 and q.is_cuda
     assert k_rows.dtype == v_rows.dtype == torch.float16 and k_rows.is_contiguous() and v_rows.is_contiguous()
     n_seq, T, n_head, hd = q.shape
     assert state.dtype == torch.float32 and state.numel() == n_seq * T * n_head * (hd + 2)
+    assert out is None or (out.dtype == q.dtype and out.shape == q.shape)
     desc = make_desc(n_head, n_kv, hd, n_seq=n_seq, q_tokens=T, kv_len=kv_len, kv_row_stride=kv_row_stride,
-                     window=window, scale=scale)
+                     window=window, scale=scale, q_token_stride=token_stride(q),
+                     out_token_stride=0 if out is None else token_stride(out))
     lib = load_library()
-    _check(lib.pelica_attn_prefill_round(ctypes.byref(desc), _ptr(q), _ptr(k_rows), _ptr(v_rows), key_begin,
-                                         key_end, _ptr(sinks), _ptr(state), 1 if first else 0, _ptr(out),
-                                         _stream_ptr(stream)))
+    fn = lib.pelica_attn_prefill_round if q.dtype == torch.float16 else lib.pelica_attn_prefill_round_f32
+    _check(fn(ctypes.byref(desc), _ptr(q), _ptr(k_rows), _ptr(v_rows), key_begin, key_end, _ptr(sinks), _ptr(state),
+              1 if first else 0, _ptr(out), _stream_ptr(stream)))
     return out
 
 

@@ -42,8 +42,6 @@ struct Tuning {
     int decode_waves;   // PELICA_ATTN_DECODE_WAVES (target waves of a split grid)
     int sk_restart;     // PELICA_ATTN_SK_RESTART (positions charged per stream-K piece start)
     int mla_workgroups; // PELICA_ATTN_MLA_WORKGROUPS
-    int fuse;           // PELICA_ATTN_FUSE (in-kernel split merge; default 0)
-    int fuse_groups;    // PELICA_ATTN_FUSE_GROUPS (level-1 groups; default 8)
 };
 
 Tuning read_tuning() {
@@ -53,17 +51,23 @@ Tuning read_tuning() {
     x.decode_waves = std::max(0, env_int("PELICA_ATTN_DECODE_WAVES", 0));
     x.sk_restart = env_int("PELICA_ATTN_SK_RESTART", -1);
     x.mla_workgroups = std::max(0, env_int("PELICA_ATTN_MLA_WORKGROUPS", 0));
-    x.fuse = env_int("PELICA_ATTN_FUSE", 0);
-    x.fuse_groups = std::max(1, env_int("PELICA_ATTN_FUSE_GROUPS", 8));
     return x;
 }
 
-Tuning& tuning_slot() {
-    static Tuning t = read_tuning();
-    return t;
-}
+// Published as an immutable object through an atomic pointer, so a reload
+// never races a planning call; a replaced object is kept (a planning call
+// may still read it), a few bytes per reload.
+std::atomic<const Tuning*> g_tuning{nullptr};
 
-const Tuning& tuning() { return tuning_slot(); }
+const Tuning& tuning() {
+    const Tuning* t = g_tuning.load(std::memory_order_acquire);
+    if (!t) {
+        const Tuning* fresh = new Tuning(read_tuning());
+        if (g_tuning.compare_exchange_strong(t, fresh, std::memory_order_acq_rel)) t = fresh;
+        else delete fresh;  // another thread published first: t is its object
+    }
+    return *t;
+}
 
 bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) != 0; }
 
@@ -125,21 +129,36 @@ int check_desc(const PelicaAttnDesc* d, bool mla = false) {
     return PELICA_ATTN_OK;
 }
 
+// Token strides of q and out (values of q_es / o_es bytes): 0 or at least a
+// token's heads, keeping every token's rows 16-byte aligned, and below 2^20
+// values (the kernels address a block of tokens with 32-bit byte offsets).
+int check_strides(const PelicaAttnDesc* d, int q_es, int o_es) {
+    const int64_t row = (int64_t)d->n_head * d->hd;
+    auto bad = [&](int64_t st, int es) { return st != 0 && (st < row || st >= (1 << 20) || (st * es) % 16); };
+    if (bad(d->q_token_stride, q_es))
+        return fail(PELICA_ATTN_EINVAL, "q_token_stride %lld: 0, or >= n_head*hd (%lld), < 2^20 and a whole number of "
+                    "16-byte pieces", (long long)d->q_token_stride, (long long)row);
+    if (bad(d->out_token_stride, o_es))
+        return fail(PELICA_ATTN_EINVAL, "out_token_stride %lld: 0, or >= n_head*hd (%lld), < 2^20 and a whole number "
+                    "of 16-byte pieces", (long long)d->out_token_stride, (long long)row);
+    return PELICA_ATTN_OK;
+}
+
+int64_t q_stride(const PelicaAttnDesc* d) { return d->q_token_stride ? d->q_token_stride : (int64_t)d->n_head * d->hd; }
+int64_t o_stride(const PelicaAttnDesc* d) { return d->out_token_stride ? d->out_token_stride : (int64_t)d->n_head * d->hd; }
+
 float eff_scale(const PelicaAttnDesc* d) { return d->scale > 0.f ? d->scale : 1.f / std::sqrt((float)d->hd); }
 
 struct DecodePlan {
     int R, rt, n_rg, split_keys, n_slot, wg_heads, nw;
     bool sk;
     int sk_grid, sk_minb, sk_restart;
-    bool fuse;
-    int n_grp;
-    size_t ctr_bytes, ml_bytes, o_bytes, l1ml_bytes, ws_bytes;
+    size_t ctr_bytes, ml_bytes, o_bytes, ws_bytes;
 };
 
-// allow_fuse: the in-kernel split merge may be planned (its counters need a
-// workspace zero-filled before the first call; the no-allocation entry point
-// never uses it)
-int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl, bool allow_fuse = true) {
+// kr_len: keys of the call's key range (pelica_attn_decode_partials_range),
+// 0 for the whole cache
+int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl, int kr_len = 0) {
     int rc = check_desc(d);
     if (rc) return rc;
     const Tuning& tn = tuning();
@@ -152,6 +171,11 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl, bool allow_fuse = true)
     // keys any row of a sequence can see
     const long long span = d->window > 0 ? std::min<long long>(d->kv_len, (long long)d->window + d->q_tokens - 1)
                                          : d->kv_len;
+    // A key range plans the splits of the whole cache (the same split size,
+    // so its workspace is never larger than pelica_attn_workspace_bytes
+    // gives) and keeps the splits that hold its keys.
+    const long long span_r = kr_len > 0 ? std::min<long long>(span, kr_len) : span;
+    const bool bounded = d->window > 0 || kr_len > 0;
     const long long groups = (long long)d->n_seq * d->n_kv * n_rg;
     const long long blocks = (long long)ceil_div(span, 64) * groups;
     // Workgroup shape.  Large head-dim-64 calls: 8 waves, 4 kv heads per
@@ -180,7 +204,7 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl, bool allow_fuse = true)
         int n_slot = 0;
         for (;;) {
             const int total = ceil_div(d->kv_len, split_keys);
-            n_slot = d->window > 0 ? std::min<int>(total, ceil_div(span, split_keys) + 1) : total;
+            n_slot = bounded ? std::min<int>(total, ceil_div(span_r, split_keys) + 1) : total;
             if (n_slot <= pelica::kMaxSlots) break;
             split_keys *= 2;
         }
@@ -240,19 +264,11 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl, bool allow_fuse = true)
     // workspace: (max, sum) pairs, then O rows, 256-byte aligned parts
     const size_t n_part = (size_t)d->n_seq * d->n_kv * R * n_slot;
     auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
-    // (the fused merge addresses its partials with 31-bit byte offsets)
-    pl->fuse = allow_fuse && !sk && n_slot > 1 && tn.fuse && (size_t)d->n_seq * d->n_kv * R * n_slot * d->hd * 4 < (1u << 31);
-    pl->n_grp = pl->fuse ? std::min(tn.fuse_groups, n_slot) : 0;
-    const size_t segs = (size_t)d->n_seq * (d->n_kv / wg_heads) * n_rg;
-    // stream-K: the piece count of each segment; fused merge: the arrival
-    // counters; then the partials (and the fused merge's level-1 partials)
-    pl->ctr_bytes = sk ? al((size_t)d->n_seq * d->n_kv * n_rg * 4) : pl->fuse ? al(segs * (pl->n_grp + 1) * 4) : 0;
+    // stream-K: the piece count of each segment, then the partials
+    pl->ctr_bytes = sk ? al((size_t)d->n_seq * d->n_kv * n_rg * 4) : 0;
     pl->ml_bytes = al(n_part * 2 * 4);
     pl->o_bytes = al(n_part * d->hd * 4);
-    const size_t n_l1 = (size_t)d->n_seq * d->n_kv * R * pl->n_grp;
-    pl->l1ml_bytes = al(n_l1 * 2 * 4);
-    pl->ws_bytes = n_slot > 1 ? pl->ctr_bytes + pl->ml_bytes + pl->o_bytes + (pl->fuse ? pl->l1ml_bytes + n_l1 * d->hd * 4 : 0)
-                              : 0;
+    pl->ws_bytes = n_slot > 1 ? pl->ctr_bytes + pl->ml_bytes + pl->o_bytes : 0;
     return PELICA_ATTN_OK;
 }
 
@@ -302,7 +318,7 @@ int pelica_attn_version(void) { return PELICA_ATTN_VERSION; }
 
 int pelica_attn_reload_tuning(void) {
     g_err[0] = 0;
-    tuning_slot() = read_tuning();
+    g_tuning.store(new Tuning(read_tuning()), std::memory_order_release);
     return PELICA_ATTN_OK;
 }
 
@@ -330,12 +346,15 @@ int pelica_attn_workspace_init(void* workspace, size_t workspace_bytes, void* st
 namespace {
 
 // decode into out (final, with sinks) or into merge_dec partial slots
+// key_end > 0: keys [key_begin, key_end) only, cache row 0 = position key_begin
 int run_decode(const PelicaAttnDesc* desc, const float* q, const uint16_t* k, const uint16_t* v,
                const float* sinks, float* out, float* parts, void* workspace, size_t workspace_bytes,
-               void* stream, bool allow_fuse = true) {
+               void* stream, int key_begin = 0, int key_end = 0) {
     g_err[0] = 0;
     DecodePlan pl;
-    int rc = plan_decode(desc, &pl, allow_fuse);
+    int rc = plan_decode(desc, &pl, key_end > 0 ? key_end - key_begin : 0);
+    if (rc) return rc;
+    rc = check_strides(desc, 4, 4);
     if (rc) return rc;
     if (!q || !k || !v || !(out || parts))
         return fail(PELICA_ATTN_EINVAL, "q, k, v and %s must be non-NULL", parts ? "parts" : "out");
@@ -358,6 +377,10 @@ int run_decode(const PelicaAttnDesc* desc, const float* q, const uint16_t* k, co
     p.seq_len = desc->seq_kv_len;
     p.seq_off = desc->seq_kv_offset;
     p.row_stride = desc->kv_row_stride ? desc->kv_row_stride : (int64_t)desc->n_kv * desc->hd;
+    p.q_tok = q_stride(desc);
+    p.o_tok = o_stride(desc);
+    p.kr_lo = key_end > 0 ? key_begin : 0;
+    p.kr_hi = key_end > 0 ? key_end : INT32_MAX;
     p.kv_len = desc->kv_len;
     p.n_head = desc->n_head;
     p.n_kv = desc->n_kv;
@@ -381,15 +404,6 @@ int run_decode(const PelicaAttnDesc* desc, const float* q, const uint16_t* k, co
     p.sk_restart = pl.sk_restart;
     p.rg_rows = 16 * pl.rt;
     p.ws_np = pl.sk && pl.ws_bytes ? reinterpret_cast<int*>(ws) : nullptr;
-    p.fuse = pl.fuse;
-    if (pl.fuse) {
-        const size_t segs = (size_t)desc->n_seq * (desc->n_kv / pl.wg_heads) * pl.n_rg;
-        p.n_grp = pl.n_grp;
-        p.ctr1 = reinterpret_cast<unsigned*>(ws);
-        p.ctr2 = p.ctr1 + segs * pl.n_grp;
-        p.l1_ml = reinterpret_cast<float*>(ws + pl.ctr_bytes + pl.ml_bytes + pl.o_bytes);
-        p.l1_o = reinterpret_cast<float*>(ws + pl.ctr_bytes + pl.ml_bytes + pl.o_bytes + pl.l1ml_bytes);
-    }
     hipError_t e = pelica::launch_decode(p, pl.rt, pl.nw, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(PELICA_ATTN_EHIP, "decode launch: %s", hipGetErrorString(e));
     return PELICA_ATTN_OK;
@@ -427,6 +441,73 @@ int scratch_of_current_device(void** out) {
     return PELICA_ATTN_OK;
 }
 
+// One round of a prompt's keys (pelica_attn_prefill_round): key positions
+// [key_begin, key_end) in rows from row 0, folded into state
+struct Round {
+    int32_t key_begin, key_end;
+    float* state;
+    int32_t first;
+};
+
+// prefill over the whole cache (round == NULL) or one round of keys; f32:
+// f32 queries and output, else f16
+int run_prefill(const PelicaAttnDesc* desc, const void* q, const uint16_t* k, const uint16_t* v, const float* sinks,
+                void* out, bool f32, const Round* round, void* stream) {
+    g_err[0] = 0;
+    int rc = check_desc(desc);
+    if (rc) return rc;
+    const int es = f32 ? 4 : 2;
+    rc = check_strides(desc, es, es);
+    if (rc) return rc;
+    if (desc->flags) return fail(PELICA_ATTN_EINVAL, "flags must be 0");
+    if (round) {
+        if (desc->n_seq != 1 || desc->ring_cap || desc->seq_kv_len)
+            return fail(PELICA_ATTN_EINVAL, "rounds take one sequence of a linear cache");
+        if (!q || !k || !v || !round->state)
+            return fail(PELICA_ATTN_EINVAL, "q, k_rows, v_rows and state must be non-NULL");
+        if (reinterpret_cast<uintptr_t>(round->state) % 4) return fail(PELICA_ATTN_EINVAL, "state must be 4-byte aligned");
+        if (round->key_begin < 0 || round->key_end <= round->key_begin || round->key_end > desc->kv_len)
+            return fail(PELICA_ATTN_EINVAL, "round [%d, %d) outside the %d keys", round->key_begin, round->key_end,
+                        desc->kv_len);
+    } else if (!q || !k || !v || !out) {
+        return fail(PELICA_ATTN_EINVAL, "q, k, v and out must be non-NULL");
+    }
+    if (misaligned(q) || misaligned(k) || misaligned(v) || misaligned(out))
+        return fail(PELICA_ATTN_EINVAL, "q, k, v and out must be 16-byte aligned");
+    pelica::PrefillParams p{};
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.sinks = sinks;
+    p.out = out;
+    p.f32 = f32;
+    p.q_tok = q_stride(desc);
+    p.o_tok = o_stride(desc);
+    p.seq_len = round ? nullptr : desc->seq_kv_len;
+    p.seq_off = round ? nullptr : desc->seq_kv_offset;
+    p.row_stride = desc->kv_row_stride ? desc->kv_row_stride : (int64_t)desc->n_kv * desc->hd;
+    p.kv_len = desc->kv_len;
+    p.n_head = desc->n_head;
+    p.n_kv = desc->n_kv;
+    p.hd = desc->hd;
+    p.hpk = desc->n_head / desc->n_kv;
+    p.T = desc->q_tokens;
+    p.n_seq = desc->n_seq;
+    p.window = desc->window;
+    p.ring_cap = round ? 0 : desc->ring_cap;
+    p.qscale = eff_scale(desc) * pelica::kLog2e;
+    if (round) {
+        p.key_begin = round->key_begin;
+        p.key_end = round->key_end;
+        p.first = round->first ? 1 : 0;
+        p.state = round->state;
+    }
+    hipError_t e = pelica::launch_prefill(p, static_cast<hipStream_t>(stream));
+    if (e == hipErrorNotSupported) return fail(PELICA_ATTN_EUNSUPPORTED, "prefill shape unsupported");
+    if (e != hipSuccess) return fail(PELICA_ATTN_EHIP, "prefill launch: %s", hipGetErrorString(e));
+    return PELICA_ATTN_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -435,7 +516,7 @@ int pelica_attn_decode_noalloc(const PelicaAttnDesc* desc, const float* q, const
                                const float* sinks, float* out, void* stream) {
     g_err[0] = 0;
     DecodePlan pl;
-    int rc = plan_decode(desc, &pl, false);
+    int rc = plan_decode(desc, &pl);
     if (rc) return rc;
     if (desc->flags) return fail(PELICA_ATTN_EINVAL, "flags must be 0");
     if (pl.ws_bytes > PELICA_ATTN_NOALLOC_SCRATCH_BYTES)
@@ -448,7 +529,7 @@ int pelica_attn_decode_noalloc(const PelicaAttnDesc* desc, const float* q, const
         if (rc) return rc;
     }
     return run_decode(desc, q, k, v, sinks, out, nullptr, ws, pl.ws_bytes ? PELICA_ATTN_NOALLOC_SCRATCH_BYTES : 0,
-                      stream, false);
+                      stream);
 }
 
 int pelica_attn_decode(const PelicaAttnDesc* desc, const float* q, const uint16_t* k, const uint16_t* v,
@@ -464,6 +545,21 @@ int pelica_attn_decode_partials(const PelicaAttnDesc* desc, const float* q, cons
         return fail(PELICA_ATTN_EINVAL, "parts must be non-NULL");
     }
     return run_decode(desc, q, k, v, nullptr, nullptr, parts, workspace, workspace_bytes, stream);
+}
+
+int pelica_attn_decode_partials_range(const PelicaAttnDesc* desc, const float* q, const uint16_t* k_rows,
+                                      const uint16_t* v_rows, int32_t key_begin, int32_t key_end, float* parts,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
+    g_err[0] = 0;
+    if (!desc) return fail(PELICA_ATTN_EINVAL, "desc is NULL");
+    if (!parts) return fail(PELICA_ATTN_EINVAL, "parts must be non-NULL");
+    if (desc->n_seq != 1 || desc->seq_kv_len || desc->seq_kv_offset || desc->ring_cap)
+        return fail(PELICA_ATTN_EINVAL, "a key range takes one sequence of a linear cache (n_seq 1, no seq_kv_len / "
+                    "seq_kv_offset, ring_cap 0)");
+    if (key_begin < 0 || key_end <= key_begin || key_end > desc->kv_len)
+        return fail(PELICA_ATTN_EINVAL, "key range [%d, %d) outside the %d keys", key_begin, key_end, desc->kv_len);
+    return run_decode(desc, q, k_rows, v_rows, nullptr, nullptr, parts, workspace, workspace_bytes, stream, key_begin,
+                      key_end);
 }
 
 int pelica_attn_qkv_rope_cache(const PelicaAttnDesc* desc, const PelicaRope* rope, float* q, const float* k,
@@ -529,40 +625,6 @@ int pelica_attn_qkv_rope_cache(const PelicaAttnDesc* desc, const PelicaRope* rop
     return PELICA_ATTN_OK;
 }
 
-int pelica_attn_prefill(const PelicaAttnDesc* desc, const uint16_t* q, const uint16_t* k, const uint16_t* v,
-                        const float* sinks, uint16_t* out, void* stream) {
-    g_err[0] = 0;
-    int rc = check_desc(desc);
-    if (rc) return rc;
-    if (desc->flags) return fail(PELICA_ATTN_EINVAL, "flags must be 0");
-    if (!q || !k || !v || !out) return fail(PELICA_ATTN_EINVAL, "q, k, v and out must be non-NULL");
-    if (misaligned(q) || misaligned(k) || misaligned(v) || misaligned(out))
-        return fail(PELICA_ATTN_EINVAL, "q, k, v and out must be 16-byte aligned");
-    pelica::PrefillParams p{};
-    p.q = q;
-    p.k = k;
-    p.v = v;
-    p.sinks = sinks;
-    p.out = out;
-    p.seq_len = desc->seq_kv_len;
-    p.seq_off = desc->seq_kv_offset;
-    p.row_stride = desc->kv_row_stride ? desc->kv_row_stride : (int64_t)desc->n_kv * desc->hd;
-    p.kv_len = desc->kv_len;
-    p.n_head = desc->n_head;
-    p.n_kv = desc->n_kv;
-    p.hd = desc->hd;
-    p.hpk = desc->n_head / desc->n_kv;
-    p.T = desc->q_tokens;
-    p.n_seq = desc->n_seq;
-    p.window = desc->window;
-    p.ring_cap = desc->ring_cap;
-    p.qscale = eff_scale(desc) * pelica::kLog2e;
-    hipError_t e = pelica::launch_prefill(p, static_cast<hipStream_t>(stream));
-    if (e == hipErrorNotSupported) return fail(PELICA_ATTN_EUNSUPPORTED, "prefill shape unsupported");
-    if (e != hipSuccess) return fail(PELICA_ATTN_EHIP, "prefill launch: %s", hipGetErrorString(e));
-    return PELICA_ATTN_OK;
-}
-
 size_t pelica_attn_mla_workspace_bytes(const PelicaAttnDesc* desc) {
     g_err[0] = 0;
     DecodePlan pl;
@@ -575,6 +637,8 @@ int pelica_attn_mla(const PelicaAttnDesc* desc, const float* q, const uint16_t* 
     g_err[0] = 0;
     DecodePlan pl;
     int rc = plan_mla(desc, &pl);
+    if (rc) return rc;
+    rc = check_strides(desc, 4, 4);
     if (rc) return rc;
     if (desc->flags) return fail(PELICA_ATTN_EINVAL, "flags must be 0");
     if (!q || !latent || !out) return fail(PELICA_ATTN_EINVAL, "q, latent and out must be non-NULL");
@@ -594,6 +658,10 @@ int pelica_attn_mla(const PelicaAttnDesc* desc, const float* q, const uint16_t* 
     p.seq_len = desc->seq_kv_len;
     p.seq_off = desc->seq_kv_offset;
     p.row_stride = desc->kv_row_stride ? desc->kv_row_stride : 512;
+    p.q_tok = q_stride(desc);
+    p.o_tok = o_stride(desc);
+    p.kr_lo = 0;
+    p.kr_hi = INT32_MAX;
     p.kv_len = desc->kv_len;
     p.n_head = desc->n_head;
     p.n_kv = 1;
@@ -613,45 +681,28 @@ int pelica_attn_mla(const PelicaAttnDesc* desc, const float* q, const uint16_t* 
     return PELICA_ATTN_OK;
 }
 
+int pelica_attn_prefill(const PelicaAttnDesc* desc, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                        const float* sinks, uint16_t* out, void* stream) {
+    return run_prefill(desc, q, k, v, sinks, out, false, nullptr, stream);
+}
+
+int pelica_attn_prefill_f32(const PelicaAttnDesc* desc, const float* q, const uint16_t* k, const uint16_t* v,
+                            const float* sinks, float* out, void* stream) {
+    return run_prefill(desc, q, k, v, sinks, out, true, nullptr, stream);
+}
+
 int pelica_attn_prefill_round(const PelicaAttnDesc* desc, const uint16_t* q, const uint16_t* k_rows,
                               const uint16_t* v_rows, int32_t key_begin, int32_t key_end, const float* sinks,
                               float* state, int32_t first, uint16_t* out, void* stream) {
-    g_err[0] = 0;
-    int rc = check_desc(desc);
-    if (rc) return rc;
-    if (desc->flags) return fail(PELICA_ATTN_EINVAL, "flags must be 0");
-    if (desc->n_seq != 1 || desc->ring_cap || desc->seq_kv_len)
-        return fail(PELICA_ATTN_EINVAL, "rounds take one sequence of a linear cache");
-    if (!q || !k_rows || !v_rows || !state) return fail(PELICA_ATTN_EINVAL, "q, k_rows, v_rows and state must be non-NULL");
-    if (misaligned(q) || misaligned(k_rows) || misaligned(v_rows) || misaligned(out))
-        return fail(PELICA_ATTN_EINVAL, "q, k_rows, v_rows and out must be 16-byte aligned");
-    if (reinterpret_cast<uintptr_t>(state) % 4) return fail(PELICA_ATTN_EINVAL, "state must be 4-byte aligned");
-    if (key_begin < 0 || key_end <= key_begin || key_end > desc->kv_len)
-        return fail(PELICA_ATTN_EINVAL, "round [%d, %d) outside the %d keys", key_begin, key_end, desc->kv_len);
-    pelica::PrefillParams p{};
-    p.q = q;
-    p.k = k_rows;
-    p.v = v_rows;
-    p.sinks = sinks;
-    p.out = out;
-    p.row_stride = desc->kv_row_stride ? desc->kv_row_stride : (int64_t)desc->n_kv * desc->hd;
-    p.kv_len = desc->kv_len;
-    p.n_head = desc->n_head;
-    p.n_kv = desc->n_kv;
-    p.hd = desc->hd;
-    p.hpk = desc->n_head / desc->n_kv;
-    p.T = desc->q_tokens;
-    p.n_seq = 1;
-    p.window = desc->window;
-    p.qscale = eff_scale(desc) * pelica::kLog2e;
-    p.key_begin = key_begin;
-    p.key_end = key_end;
-    p.first = first ? 1 : 0;
-    p.state = state;
-    hipError_t e = pelica::launch_prefill(p, static_cast<hipStream_t>(stream));
-    if (e == hipErrorNotSupported) return fail(PELICA_ATTN_EUNSUPPORTED, "prefill shape unsupported");
-    if (e != hipSuccess) return fail(PELICA_ATTN_EHIP, "prefill launch: %s", hipGetErrorString(e));
-    return PELICA_ATTN_OK;
+    const Round r{key_begin, key_end, state, first};
+    return run_prefill(desc, q, k_rows, v_rows, sinks, out, false, &r, stream);
+}
+
+int pelica_attn_prefill_round_f32(const PelicaAttnDesc* desc, const float* q, const uint16_t* k_rows,
+                                  const uint16_t* v_rows, int32_t key_begin, int32_t key_end, const float* sinks,
+                                  float* state, int32_t first, float* out, void* stream) {
+    const Round r{key_begin, key_end, state, first};
+    return run_prefill(desc, q, k_rows, v_rows, sinks, out, true, &r, stream);
 }
 
 int pelica_attn_partials_merge_batch(int32_t n_tokens, int32_t n_head, int32_t hd, int32_t n_parts,

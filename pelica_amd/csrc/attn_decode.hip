@@ -76,19 +76,6 @@ __device__ __forceinline__ float wave_sum(float x) {
 template <int HD, int RT, int NW>
 constexpr int kDecodeOcc = NW == 8 ? 2 : (NW == 4 && HD == 64 && RT <= 2) ? 2 : 1;
 
-// f16 parts the decode kernel splits Q and P into: 2 (hi + lo, ~fp32
-// products) or 1 (f16 only)
-#ifndef PELICA_DECODE_PARTS
-#define PELICA_DECODE_PARTS 2
-#endif
-constexpr int kDecodeSplitParts = PELICA_DECODE_PARTS;
-
-// cache policy bits of the K/V stream loads: nt (streaming, the cache lines
-// are not kept) — each K/V byte is read once
-#ifndef PELICA_DECODE_AUX
-#define PELICA_DECODE_AUX 2
-#endif
-constexpr int kKvAux = PELICA_DECODE_AUX;
 
 // word 3 of a gfx9 buffer resource: 32-bit data format, raw addressing
 constexpr int kBufferFlags = 0x00020000;
@@ -98,9 +85,13 @@ struct KeyRange {
     int lo, pos;
 };
 
-__device__ __forceinline__ KeyRange key_range(int len, int T, int t, int window) {
-    const int pos = len - T + t;
-    return KeyRange{(window > 0 && pos + 1 > window) ? pos + 1 - window : 0, pos};
+// Keys query token t of a sequence of len keys sees: [lo, pos] under the
+// window, clipped to the call's key range [kr_lo, kr_hi) (the whole cache
+// unless the call covers one range of positions)
+__device__ __forceinline__ KeyRange key_range(const DecodeParams& p, int len, int t) {
+    const int pos = len - p.T + t;
+    const int lo = (p.window > 0 && pos + 1 > p.window) ? pos + 1 - p.window : 0;
+    return KeyRange{max(lo, p.kr_lo), min(pos, p.kr_hi - 1)};
 }
 
 // LDS byte offset of 16-byte piece p of key row k in a V block: rows of HD
@@ -165,10 +156,9 @@ __device__ constexpr int k_swz_j(int j) {
 // compiler does not track it (loads inside the block loop, whose waits are
 // counted by hand; lds_dma16_untracked)
 __device__ __forceinline__ void kv_dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset, char* lds, bool tracked) {
-    if (tracked) lds_dma16<kKvAux == 2>(rsrc, voffset, lds);
-    else lds_dma16_untracked<kKvAux == 2>(rsrc, voffset, lds);
+    if (tracked) lds_dma16<true>(rsrc, voffset, lds);
+    else lds_dma16_untracked<true>(rsrc, voffset, lds);
 }
-static_assert(kKvAux == 0 || kKvAux == 2, "K/V cache policy: default or nt");
 
 // s_waitcnt vmcnt(N), the other counters left alone (gfx9 encoding)
 template <int N>
@@ -272,153 +262,6 @@ __device__ SkLayout sk_layout(const DecodeParams& p, int gy, const SeqTables& tb
     return L;
 }
 
-// Device-coherent (agent-scope) accesses of the fused merge's partials: the
-// sc1 cache policy writes a store through to the device's coherence point and
-// makes a load miss any stale copy in this CU's L1 and this XCD's L2 — the
-// same accesses the compiler emits for relaxed agent-scope atomic loads and
-// stores, at 16 bytes a lane.  Ordering comes from waiting for the stores
-// (vmcnt) before the arrival counter's atomic, and from issuing the loads
-// after the atomic has returned.  (An acq_rel counter instead writes back and
-// invalidates the whole L2 per workgroup; measured ~12 us slower on the 32K
-// gpt-oss layer.)
-constexpr int kAuxDev = 16;  // sc1
-// a buffer resource over a wave-uniform base (per-lane bases would make every
-// access a waterfall loop); offsets are in bytes, below 2^31
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const void* base) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, kBufferFlags);
-}
-__device__ __forceinline__ void st_dev4(const __amdgpu_buffer_rsrc_t& r, size_t off, const float4v& v) {
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, (int)off, 0, kAuxDev);
-}
-__device__ __forceinline__ void st_dev2(const __amdgpu_buffer_rsrc_t& r, size_t off, const float2& v) {
-    __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(v.x), __float_as_uint(v.y)}, r, (int)off, 0, kAuxDev);
-}
-__device__ __forceinline__ float4v ld_dev4(const __amdgpu_buffer_rsrc_t& r, size_t off) {
-    return __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kAuxDev));
-}
-__device__ __forceinline__ float2 ld_dev2(const __amdgpu_buffer_rsrc_t& r, size_t off) {
-    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, kAuxDev);
-    return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
-}
-
-// slots a merging thread loads before merging them
-constexpr int kFuseBatch = 16;
-
-// (m, l, o) := (m, l, o) merged with (m2, l2, o2), base-2 maxima
-__device__ __forceinline__ void merge_state(float& m, float& l, float4v& o, float m2, float l2, const float4v& o2) {
-    const float M = fmaxf(m, m2);
-    const float ms = (M == -INFINITY) ? 0.f : M;
-    const float a = fast_exp2(m - ms), b = fast_exp2(m2 - ms);
-    l = l * a + l2 * b;
-    o = o * a + o2 * b;
-    m = M;
-}
-
-// sink in max and denominator, then 1/L (or 1/L alone): the output factor
-// of a row's merged state (m base-2 max, l sum)
-__device__ __forceinline__ float out_factor(const DecodeParams& p, int h, float m, float l) {
-    if (!p.sinks) return 1.f / l;
-    const float sk = p.sinks[h] * kLog2e;
-    const float M2 = fmaxf(m, sk);
-    const float ms = (m == -INFINITY) ? 0.f : m;
-    const float wgt = fast_exp2(ms - M2);
-    return wgt / (l * wgt + fast_exp2(sk - M2));
-}
-
-// In-kernel merge of the key splits, after this workgroup's split partials
-// are stored (see DecodeParams::fuse).  Level 1: the splits of group
-// slot % n_grp; level 2: the groups in order.  Each level's last arriver is
-// found with an agent-scope acq_rel counter: its release makes this
-// workgroup's partials (ordered before it by the barrier) visible across
-// the XCDs' L2s, its acquire makes the other workgroups' partials visible
-// to this one.  The merging threads take (row, 4 dims) items of the
-// workgroup's wg_heads kv heads.
-template <int HD, int H>
-__device__ __forceinline__ void fused_merge(const DecodeParams& p, int s, int by, int len, int slot, int n_active,
-                                         int* s_last) {
-    const int tid = threadIdx.x, nt = blockDim.x;
-    const int hgroups = p.n_kv / H, rg = by / hgroups, kv0 = (by % hgroups) * H;
-    const int rows = min(p.rg_rows, p.R - rg * p.rg_rows);  // this row group's rows
-    const int rbase = rg * p.rg_rows;
-    constexpr int Q = HD / 4;
-    const int items = H * rows * Q;
-    const int grp = slot % p.n_grp;
-    const int n_g = min(p.n_grp, n_active);            // groups with a split
-    const int cnt = (n_active - grp + p.n_grp - 1) / p.n_grp;  // splits of this group
-    wait_vm<0>();  // this wave's partial stores are done
-    __syncthreads();
-    if (tid == 0) {
-        unsigned* c = p.ctr1 + ((size_t)s * hgroups * p.n_rg + by) * p.n_grp + grp;
-        const unsigned old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const bool last = old + 1 == (unsigned)cnt;
-        if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *s_last = last;
-    }
-    __syncthreads();
-    if (!*s_last) return;
-    // level 1: this group's splits in slot order
-    for (int it = tid; it < items; it += nt) {
-        const int q4 = it % Q, rr = (it / Q) % rows, hl = it / (Q * rows);
-        const int r = rbase + rr, kvh = kv0 + hl;
-        const size_t base = ((size_t)(s * p.n_kv + kvh) * p.R + r) * p.n_slot;
-        float m = -INFINITY, l = 0.f;
-        float4v o = {0.f, 0.f, 0.f, 0.f};
-        for (int c0 = grp; c0 < n_active; c0 += kFuseBatch * p.n_grp) {
-            float2 ml[kFuseBatch];
-            float4v ov[kFuseBatch];
-#pragma unroll
-            for (int j = 0; j < kFuseBatch; ++j) {  // all loads in flight, then the merge
-                const int c = c0 + j * p.n_grp;
-                ml[j] = c < n_active ? ld_dev2(dev_rsrc(p.ws_ml), 8 * (base + c)) : make_float2(-INFINITY, 0.f);
-                ov[j] = c < n_active ? ld_dev4(dev_rsrc(p.ws_o), 4 * ((base + c) * HD + 4 * q4)) : float4v{0.f, 0.f, 0.f, 0.f};
-            }
-#pragma unroll
-            for (int j = 0; j < kFuseBatch; ++j) merge_state(m, l, o, ml[j].x, ml[j].y, ov[j]);
-        }
-        const size_t g1 = ((size_t)(s * p.n_kv + kvh) * p.R + r) * p.n_grp + grp;
-        if (q4 == 0) st_dev2(dev_rsrc(p.l1_ml), 8 * g1, make_float2(m, l));
-        st_dev4(dev_rsrc(p.l1_o), 4 * (g1 * HD + 4 * q4), o);
-    }
-    wait_vm<0>();
-    __syncthreads();
-    if (tid == 0) {
-        unsigned* c = p.ctr2 + (size_t)s * hgroups * p.n_rg + by;
-        const unsigned old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const bool last = old + 1 == (unsigned)n_g;
-        if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *s_last = last;
-    }
-    __syncthreads();
-    if (!*s_last) return;
-    // level 2: the groups in order, the sink, the output
-    for (int it = tid; it < items; it += nt) {
-        const int q4 = it % Q, rr = (it / Q) % rows, hl = it / (Q * rows);
-        const int r = rbase + rr, kvh = kv0 + hl;
-        const size_t base = ((size_t)(s * p.n_kv + kvh) * p.R + r) * p.n_grp;
-        float m = -INFINITY, l = 0.f;
-        float4v o = {0.f, 0.f, 0.f, 0.f};
-        for (int g0 = 0; g0 < n_g; g0 += kFuseBatch) {
-            float2 ml[kFuseBatch];
-            float4v ov[kFuseBatch];
-#pragma unroll
-            for (int j = 0; j < kFuseBatch; ++j) {
-                const int g = g0 + j;
-                ml[j] = g < n_g ? ld_dev2(dev_rsrc(p.l1_ml), 8 * (base + g)) : make_float2(-INFINITY, 0.f);
-                ov[j] = g < n_g ? ld_dev4(dev_rsrc(p.l1_o), 4 * ((base + g) * HD + 4 * q4)) : float4v{0.f, 0.f, 0.f, 0.f};
-            }
-#pragma unroll
-            for (int j = 0; j < kFuseBatch; ++j) merge_state(m, l, o, ml[j].x, ml[j].y, ov[j]);
-        }
-        const int t = r / p.hpk, h = kvh * p.hpk + r % p.hpk;
-        if (p.parts) {
-            store_part(p.parts + ((size_t)(s * p.T + t) * p.n_head + h) * (HD + 2), 4 * q4, m, l, o);
-        } else {
-            const float f = out_factor(p, h, m, l);
-            *reinterpret_cast<float4v*>(p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + 4 * q4) = o * f;
-        }
-    }
-}
-
 template <int HD, int RT, int NW, int H, bool SK>
 constexpr int kDecodeOccK = SK ? ((HD == 64 && RT == 1) ? kDecodeOcc<HD, RT, NW> : 1) : kDecodeOcc<HD, RT, NW>;
 
@@ -430,14 +273,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     constexpr int DT = HD / 16;   // 16-dim output tiles
     constexpr int VPL = HD / 8;   // 16-byte pieces per lane per block, each of K and V
     constexpr int ROWS = RT * 16;
-#ifdef PELICA_DEC_LATE_V
-    constexpr bool EARLY_V = false;
-#else
     constexpr bool EARLY_V = HD == 64 && !SK;
-#endif
-    // f16 parts of Q and P: packed (PK: hi in columns 0-7, lo in 8-15, one
-    // MFMA), or NP separate passes
-    constexpr int NP = PK ? 1 : kDecodeSplitParts;
+    // f16 parts (hi + lo) of Q and P: packed (PK: hi in columns 0-7, lo in
+    // 8-15, one MFMA), or two separate passes
+    constexpr int NP = PK ? 1 : 2;
     constexpr int BUF = 64 * HD * 2;                   // bytes of one 64-key K or V block
     constexpr int STATE = DT * RT * 64 * 16 + RT * 64 * 8;  // bytes of one wave's (O, m, l)
     // LDS per wave: a K and a V block buffer, filled straight from HBM;
@@ -446,7 +285,6 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     constexpr int SMEM = WSLOT * NW;
     __shared__ __attribute__((aligned(16))) char smem[SMEM];
     __shared__ unsigned arrivals[H];  // waves of each head done (merge at the end)
-    __shared__ int s_last;            // fused merge: this workgroup arrived last
 
     // wave index as a scalar: the buffer resources built from it stay in SGPRs
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4,
@@ -463,16 +301,18 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     auto split = [&](const int s, const int by, const int len, const int64_t row0, const int kbeg, const int kend,
                      const int slot, const bool single) {
     const int kvh = (by % hgroups) * H + hl, rg = by / hgroups;
-    const int lo_min = key_range(len, p.T, 0, p.window).lo;
+    const int lo_min = key_range(p, len, 0).lo;
     const int rbase = rg * ROWS;
 
     // ---- K/V stream setup: the first block is requested before anything
     //      else, so its HBM latency overlaps the query setup ----
     // Buffer resources over this sequence's rows of kv head kvh: 32-bit
     // offsets, and loads at offsets past num_records return 0 without
-    // touching memory — the tail of the last block costs no traffic.
+    // touching memory — the tail of the last block costs no traffic.  (A
+    // key range's rows start at position kr_lo: keys below it wrap to
+    // offsets past num_records.)
     const uint32_t stride_b = (uint32_t)p.row_stride * 2;
-    const uint32_t nrec = (RING ? (uint32_t)p.ring_cap : (uint32_t)len) * stride_b;
+    const uint32_t nrec = (RING ? (uint32_t)p.ring_cap : (uint32_t)(min(len, p.kr_hi) - p.kr_lo)) * stride_b;
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(p.k + row0 * p.row_stride + (size_t)kvh * HD), (short)0, (int)nrec, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
@@ -500,7 +340,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     auto row_of = [&](int i, int j) -> uint32_t {
         const int kb = blk(i);
         if (i >= nb) return nrec;
-        if (!RING) return (uint32_t)(kb + KPL * j + vk0) * stride_b;
+        if (!RING) return (uint32_t)(kb + KPL * j + vk0 - p.kr_lo) * stride_b;
         return (uint32_t)((kb + KPL * j + vk0) % p.ring_cap) * stride_b;
     };
     // Load j of a block fills LDS slots j*64 + lane of the wave's buffer
@@ -540,7 +380,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
         const int r = rbase + 16 * rt + (PK ? (c16 & 7) : c16);
         const int rr = r < p.R ? r : 0;
         const int t = rr / p.hpk, h = kvh * p.hpk + rr % p.hpk;
-        const float* qp = p.q + ((size_t)(s * p.T + t) * p.n_head + h) * HD + 8 * g;
+        const float* qp = p.q + (size_t)(s * p.T + t) * p.q_tok + h * HD + 8 * g;
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds) {
             qraw[rt][ds][0] = *reinterpret_cast<const float4v*>(qp + 32 * ds);
@@ -568,7 +408,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
         const bool rv_ok = r < p.R;
         const int rr = rv_ok ? r : 0;
         const int t = rr / p.hpk;
-        const KeyRange krg = key_range(len, p.T, t, p.window);
+        const KeyRange krg = key_range(p, len, t);
         posr[rt] = rv_ok ? krg.pos : -1;
         lor[rt] = krg.lo;
         if (rv_ok) {
@@ -879,21 +719,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
             } else {
                 f = 1.f / L;
             }
-            float* op = p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + 4 * g;
+            float* op = p.out + (size_t)(s * p.T + t) * p.o_tok + h * HD + 4 * g;
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<float4v*>(op + 16 * dt) = o[dt][rt] * f;
         } else {
             const size_t idx = ((size_t)(s * p.n_kv + kvh) * p.R + r) * p.n_slot + slot;
-            if (p.fuse) {
-                // device-coherent stores: another XCD's workgroup merges them
-                if (g == 0) st_dev2(dev_rsrc(p.ws_ml), 8 * idx, make_float2(M, L));
+            if (g == 0) *reinterpret_cast<float2*>(p.ws_ml + 2 * idx) = make_float2(M, L);
 #pragma unroll
-                for (int dt = 0; dt < DT; ++dt) st_dev4(dev_rsrc(p.ws_o), 4 * (idx * HD + 16 * dt + 4 * g), o[dt][rt]);
-            } else {
-                if (g == 0) *reinterpret_cast<float2*>(p.ws_ml + 2 * idx) = make_float2(M, L);
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<float4v*>(p.ws_o + idx * HD + 16 * dt + 4 * g) = o[dt][rt];
-            }
+            for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<float4v*>(p.ws_o + idx * HD + 16 * dt + 4 * g) = o[dt][rt];
         }
     }
     DTRACE(6);
@@ -903,13 +736,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
         const int slot = blockIdx.x, by = blockIdx.y, s = blockIdx.z;
         const int len = seq_keys(p.seq_len, s, p.kv_len);
         if (len < p.T || len <= 0) return;
-        const int split0 = key_range(len, p.T, 0, p.window).lo / p.split_keys;
-        const int n_active = min(p.n_slot, (len - 1) / p.split_keys - split0 + 1);
+        const int kmax = min(len, p.kr_hi);  // keys past the last one of the call
+        const int split0 = key_range(p, len, 0).lo / p.split_keys;
+        const int n_active = min(p.n_slot, (kmax - 1) / p.split_keys - split0 + 1);
         if (slot >= n_active) return;
         const int kbeg = (split0 + slot) * p.split_keys;
         const int64_t row0 = p.seq_off ? p.seq_off[s] : (int64_t)s * (p.ring_cap ? p.ring_cap : p.kv_len);
-        split(s, by, len, row0, kbeg, min(kbeg + p.split_keys, len), slot, n_active == 1);
-        if (p.fuse && n_active > 1 && !p.split_only) fused_merge<HD, H>(p, s, by, len, slot, n_active, &s_last);
+        split(s, by, len, row0, kbeg, min(kbeg + p.split_keys, kmax), slot, n_active == 1);
         return;
     }
     // stream-K: this workgroup's range of the block list, piece by piece
@@ -1015,10 +848,10 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
         c1 = p.ws_np[s * hgroups * p.n_rg + (r / p.rg_rows) * hgroups + kvh / p.wg_heads] - 1;
         if (c1 < 1) return;  // one piece: the split kernel wrote the output
     } else {
-        const int split0 = key_range(len, p.T, 0, p.window).lo / p.split_keys;
-        const int n_active = min(p.n_slot, (len - 1) / p.split_keys - split0 + 1);
+        const int split0 = key_range(p, len, 0).lo / p.split_keys;
+        const int n_active = min(p.n_slot, (min(len, p.kr_hi) - 1) / p.split_keys - split0 + 1);
         if (n_active <= 1) return;  // the split kernel wrote the output
-        const KeyRange krg = key_range(len, p.T, t, p.window);
+        const KeyRange krg = key_range(p, len, t);
         c0 = krg.lo / p.split_keys - split0;
         c1 = min(krg.pos / p.split_keys - split0, n_active - 1);
     }
@@ -1119,7 +952,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
                 const float wgt = fast_exp2(ms - M2);
                 f = wgt / (L * wgt + fast_exp2(sk - M2));
             }
-            *reinterpret_cast<float4v*>(p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + d) = O * f;
+            *reinterpret_cast<float4v*>(p.out + (size_t)(s * p.T + t) * p.o_tok + h * HD + d) = O * f;
         }
     }
 }
@@ -1150,17 +983,16 @@ static hipError_t launch_k(const DecodeParams& p, hipStream_t st) {
     }
     }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || p.n_slot == 1 || p.split_only || p.fuse) return e;
+    if (e != hipSuccess || p.n_slot == 1 || p.split_only) return e;
     return launch_combine(p, st);
 }
 
-#ifndef PELICA_COMBINE_ROW_WAVE_SLOTS
-#define PELICA_COMBINE_ROW_WAVE_SLOTS 16
-#endif
+// rows with at most this many splits take the one-wave-per-row combine
+constexpr int kCombineRowWaveSlots = 16;
 
 hipError_t launch_combine(const DecodeParams& p, hipStream_t st) {
     ProfScope ps(kProfDecodeCombine, st);
-    if (p.hd <= 128 && p.n_slot <= PELICA_COMBINE_ROW_WAVE_SLOTS) {
+    if (p.hd <= 128 && p.n_slot <= kCombineRowWaveSlots) {
         const dim3 grid((p.R + 3) / 4, p.n_kv, p.n_seq);
         if (p.hd == 64) hipLaunchKernelGGL((decode_combine_kernel<64, true, 64>), grid, dim3(256), 0, st, p);
         else hipLaunchKernelGGL((decode_combine_kernel<128, true, 128>), grid, dim3(256), 0, st, p);

@@ -23,6 +23,9 @@ struct DecodeParams {
     const int32_t* seq_len;
     const int64_t* seq_off;
     int64_t row_stride;  // f16 values between cache rows
+    int64_t q_tok, o_tok;  // f32 values between consecutive query / output tokens
+    int kr_lo, kr_hi;    // the call's key positions [kr_lo, kr_hi) (0, INT32_MAX: all);
+                         // cache row 0 holds position kr_lo
     int kv_len, n_head, n_kv, hd, hpk, T, R, n_seq, n_rg;
     int window, ring_cap;
     float qscale;        // scale * log2(e)
@@ -40,18 +43,6 @@ struct DecodeParams {
     int sk_restart;      // list positions charged at each segment's start (a piece's start-up cost)
     int* ws_np;          // stream-K: pieces of each (sequence, row group x kv head) segment
     int rg_rows;         // query rows per row group (16 x row tiles)
-    // In-kernel merge of the key splits (split grid, more than one split):
-    // the last workgroup to finish in each level-1 group of splits (slots
-    // congruent mod n_grp) merges the group's partials into l1_*, and the
-    // last group to finish merges the n_grp group results into the output.
-    // The arrival counters must be zero before the call; each call leaves
-    // them at zero.
-    bool fuse;
-    int n_grp;
-    unsigned* ctr1;      // [n_seq][n_kv / wg_heads * n_rg][n_grp]
-    unsigned* ctr2;      // [n_seq][n_kv / wg_heads * n_rg]
-    float* l1_ml;        // [n_seq][n_kv][R][n_grp] x (max, sum), base-2 max
-    float* l1_o;         // [n_seq][n_kv][R][n_grp][hd]
 };
 
 hipError_t launch_decode(const DecodeParams& p, int rt, int nw, hipStream_t st);

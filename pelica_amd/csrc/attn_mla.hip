@@ -69,10 +69,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     constexpr int DS = HD / NW / 32;             // 32-dim k-steps per wave (4)
     constexpr int DT = HD / NW / 16;             // 16-dim output tiles per wave (8)
     constexpr int ROWS = 16 * RT, NP = 2;  // f16 parts of Q (hi + lo: ~fp32 scores)
-#ifndef PELICA_MLA_P_PARTS
-#define PELICA_MLA_P_PARTS 1
-#endif
-    constexpr int NPP = PELICA_MLA_P_PARTS;  // f16 parts of P (the PV weights)
+    constexpr int NPP = 1;  // f16 parts of P (the PV weights: f16 alone is within tolerance)
     constexpr int BLK = KB * HD * 2;             // 32 KB
     constexpr int NBUF = 2;  // latent blocks in the LDS ring (two workgroups fit a CU's LDS)
     constexpr int LPB = KB / NW;                 // loads per block per thread
@@ -131,7 +128,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         qok[rt] = r < p.R;
         const int rr = qok[rt] ? r : 0;
         const int t = rr / p.hpk, h = rr % p.hpk;
-        const float* qp = p.q + ((size_t)(s * p.T + t) * p.n_head + h) * HD + 128 * wave + 8 * g;
+        const float* qp = p.q + (size_t)(s * p.T + t) * p.q_tok + h * HD + 128 * wave + 8 * g;
         posr[rt] = qok[rt] ? len - p.T + t : -1;
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds) {
@@ -329,7 +326,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const int t = r / p.hpk, h = r % p.hpk;
         if (n_active == 1) {
             const float inv = 1.f / L;
-            float* op = p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + 128 * wave + 4 * g;
+            float* op = p.out + (size_t)(s * p.T + t) * p.o_tok + h * HD + 128 * wave + 4 * g;
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<float4v*>(op + 16 * dt) = o[dt][rt] * inv;
         } else {

@@ -37,23 +37,13 @@ typedef _Float16 half2 __attribute__((ext_vector_type(2)));
 
 // word 3 of a gfx9 buffer resource: 32-bit data format, raw addressing
 constexpr int kBufferFlags = 0x00020000;
-#ifndef PELICA_SLIDE_LOAD_AUX
-#define PELICA_SLIDE_LOAD_AUX 0
-#endif
-#ifndef PELICA_SLIDE_STORE_AUX
-#define PELICA_SLIDE_STORE_AUX 2
-#endif
-#ifndef PELICA_PRE_STORE_AUX
-#define PELICA_PRE_STORE_AUX 2
-#endif
 // Cache policy of the query loads and output stores (each byte touched
 // once).  Output stores go nt (streaming), so they do not displace the K/V
 // the kv head's workgroups share in L2: the sliding-window kernel's
 // window-128 prompt 26.5-26.6 -> 23.5-24.8 us (nt query loads as well:
 // 26.9-28.1; nt query loads alone: 31.5-31.9), the full causal prompt
 // 151.9-152.3 -> 150.8-151.4 us.
-constexpr int kSlideLoadAux = PELICA_SLIDE_LOAD_AUX, kSlideStoreAux = PELICA_SLIDE_STORE_AUX;
-constexpr int kPreStoreAux = PELICA_PRE_STORE_AUX;
+constexpr int kSlideLoadAux = 0, kSlideStoreAux = 2, kPreStoreAux = 2;
 
 __device__ __forceinline__ float16v mfma32(const half8& a, const half8& b, const float16v& c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -87,13 +77,6 @@ __device__ __forceinline__ int v_slot(int k, int p) {
 
 // waves per SIMD: 2 (64 query rows per wave at hd 64, 32 at hd 128), or 1
 // with 128 rows per wave (the whole register file for one wave)
-// build switch: streaming tiles for every launch (comparison builds)
-#ifdef PELICA_PRE_NO_RESIDENT
-constexpr bool kNoResidentTiles = true;
-#else
-constexpr bool kNoResidentTiles = false;
-#endif
-
 template <int HD, int RT>
 constexpr int kPrefillOcc = HD * RT >= 256 ? 1 : 2;
 
@@ -115,7 +98,8 @@ __device__ __forceinline__ unsigned long long rtime() { return __builtin_amdgcn_
 // the workgroup's range (at most NRES of each) is requested at the start and
 // stays resident in LDS, so the chunk loop has no tile waits and no
 // barriers; otherwise tiles stream through two K and two V buffers.
-template <int HD, int RT, bool RING, bool ROUND, int NW, int NRES = 0>
+// F32: f32 queries (rounded to f16 as they are loaded) and f32 output.
+template <int HD, int RT, bool RING, bool ROUND, int NW, int NRES = 0, bool F32 = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefillOcc<HD, RT>, kPrefillOcc<HD, RT>))) void prefill_kernel(
     PrefillParams p, int n_tb, int TB) {
     constexpr int KS = HD / 16;                 // 16-dim k-steps of QK^T
@@ -232,20 +216,29 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
     half8 qb[RT][KS];
     int posr[RT], lor[RT];
     bool valid[RT];
-    const uint32_t qtok_b = (uint32_t)p.n_head * HD * 2;  // bytes of one token's query heads
+    constexpr int QES = F32 ? 4 : 2;                      // bytes per query / output value
+    const uint32_t qtok_b = (uint32_t)p.q_tok * QES;      // bytes between consecutive tokens' queries
     const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(p.q + ((size_t)s * p.T + t0) * p.n_head * HD), (short)0, (int)((uint32_t)(t1 - t0) * qtok_b),
-        kBufferFlags);
+        (void*)(static_cast<const char*>(p.q) + ((size_t)s * p.T + t0) * p.q_tok * QES), (short)0,
+        (int)((uint32_t)(t1 - t0) * qtok_b), kBufferFlags);
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
         const int r = (wave * RT + rt) * 32 + c32;
         const int t = t0 + r / p.hpk;
         valid[rt] = r < TB * p.hpk && t < t1;
         const int h = kvh * p.hpk + r % p.hpk;
-        const uint32_t qoff = valid[rt] ? (uint32_t)(t - t0) * qtok_b + (uint32_t)(h * HD + 8 * h2) * 2 : 0xFFFFFF00u;
+        const uint32_t qoff = valid[rt] ? (uint32_t)(t - t0) * qtok_b + (uint32_t)(h * HD + 8 * h2) * QES : 0xFFFFFF00u;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-            qb[rt][ks] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + 32 * ks, 0, 0));
+        for (int ks = 0; ks < KS; ++ks) {
+            if constexpr (F32) {
+                const float4v a = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + 64 * ks, 0, 0));
+                const float4v b = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + 64 * ks + 16, 0, 0));
+                qb[rt][ks] = half8{(_Float16)a[0], (_Float16)a[1], (_Float16)a[2], (_Float16)a[3],
+                                   (_Float16)b[0], (_Float16)b[1], (_Float16)b[2], (_Float16)b[3]};
+            } else {
+                qb[rt][ks] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + 32 * ks, 0, 0));
+            }
+        }
         posr[rt] = valid[rt] ? len - p.T + t : -1;
         lor[rt] = (p.window > 0 && posr[rt] + 1 > p.window) ? posr[rt] + 1 - p.window : 0;
     }
@@ -601,7 +594,24 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
 #endif
     }
 
-    if constexpr (!ROUND) {
+    if constexpr (!ROUND && F32) {
+        // f32 output: each lane stores its rows' 16-byte pieces
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            const float inv = 1.f / half_sum(l[rt]);
+            if (!valid[rt]) continue;
+            const int r = (wave * RT + rt) * 32 + c32;
+            const int t = t0 + r / p.hpk, h = kvh * p.hpk + r % p.hpk;
+            float* op = static_cast<float*>(p.out) + (size_t)(s * p.T + t) * p.o_tok + h * HD + 4 * h2;
+            // O^T lane layout: dim 32 dt + 8 (i / 4) + 4 h2 + i % 4 of row c32
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4)
+                    *reinterpret_cast<float4v*>(op + 32 * dt + 8 * i4) =
+                        float4v{o[dt][rt][4 * i4], o[dt][rt][4 * i4 + 1], o[dt][rt][4 * i4 + 2], o[dt][rt][4 * i4 + 3]} * inv;
+        }
+    } else if constexpr (!ROUND) {
         // Output through LDS: each wave writes its rows (normalised, f16)
         // into its own area, then stores whole rows — consecutive rows are
         // consecutive heads of a token, so one store instruction writes
@@ -639,10 +649,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
             const int rl = k * RPI + lane / PPR;
             val[k] = *reinterpret_cast<const u32x4*>(ow + rl * (HD * 2) + ((pc ^ (rl % PPR)) << 4));
         }
-        const uint32_t otok_b = (uint32_t)p.n_head * HD * 2;
+        const uint32_t otok_b = (uint32_t)p.o_tok * 2;
         const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(p.out + ((size_t)s * p.T + t0) * p.n_head * HD), (short)0, (int)((uint32_t)(t1 - t0) * otok_b),
-            kBufferFlags);
+            (void*)(static_cast<uint16_t*>(p.out) + ((size_t)s * p.T + t0) * p.o_tok), (short)0,
+            (int)((uint32_t)(t1 - t0) * otok_b), kBufferFlags);
 #pragma unroll
         for (int k = 0; k < NST; ++k) {
             const int r = wave * RT * 32 + k * RPI + lane / PPR;
@@ -681,14 +691,19 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kPrefil
                 inv = lt > 0.f ? inv : 0.f;
             }
         }
-        uint16_t* op = p.out + ((size_t)(s * p.T + t) * p.n_head + h) * HD + 4 * h2;
+        const size_t obase = (size_t)(s * p.T + t) * p.o_tok + h * HD + 4 * h2;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
             for (int i4 = 0; i4 < 4; ++i4) {
-                const half4 hv = {(_Float16)(o[dt][rt][4 * i4] * inv), (_Float16)(o[dt][rt][4 * i4 + 1] * inv),
-                                  (_Float16)(o[dt][rt][4 * i4 + 2] * inv), (_Float16)(o[dt][rt][4 * i4 + 3] * inv)};
-                *reinterpret_cast<half4*>(op + 32 * dt + 8 * i4) = hv;
+                const float4v ov = float4v{o[dt][rt][4 * i4], o[dt][rt][4 * i4 + 1], o[dt][rt][4 * i4 + 2],
+                                           o[dt][rt][4 * i4 + 3]} * inv;
+                if constexpr (F32) {
+                    *reinterpret_cast<float4v*>(static_cast<float*>(p.out) + obase + 32 * dt + 8 * i4) = ov;
+                } else {
+                    const half4 hv = {(_Float16)ov[0], (_Float16)ov[1], (_Float16)ov[2], (_Float16)ov[3]};
+                    *reinterpret_cast<half4*>(static_cast<uint16_t*>(p.out) + obase + 32 * dt + 8 * i4) = hv;
+                }
             }
     }
     }
@@ -777,11 +792,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         (void*)(p.k + row0 * p.row_stride + (size_t)kvh * HD), (short)0, (int)nrec, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(p.v + row0 * p.row_stride + (size_t)kvh * HD), (short)0, (int)nrec, kBufferFlags);
-    const uint32_t qtok_b = (uint32_t)p.n_head * HD * 2;  // bytes of one token's query heads
+    const uint32_t qtok_b = (uint32_t)p.q_tok * 2;  // bytes between consecutive tokens' queries
     auto q_rsrc = [&](int j) {
         const int t0 = j * TBK, t1 = min(t0 + TBK, p.T);
-        return __builtin_amdgcn_make_buffer_rsrc((void*)(p.q + ((size_t)s * p.T + t0) * p.n_head * HD), (short)0,
-                                                 (int)((uint32_t)(t1 - t0) * qtok_b), kBufferFlags);
+        return __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(static_cast<const uint16_t*>(p.q) + ((size_t)s * p.T + t0) * p.q_tok), (short)0,
+            (int)((uint32_t)(t1 - t0) * qtok_b), kBufferFlags);
     };
     // chunks [first, last] of block j: keys a row of the block sees
     auto chunk_lo = [&](int j) { return max(0, qoff0 + j * TBK + 1 - p.window) >> 5; };
@@ -876,10 +892,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const int rl = k * RPI + lane / PPR;
             val[k] = *reinterpret_cast<const u32x4*>(stage + rl * (HD * 2) + ((pc ^ (rl % PPR)) << 4));
         }
-        const uint32_t otok_b = (uint32_t)p.n_head * HD * 2;
+        const uint32_t otok_b = (uint32_t)p.o_tok * 2;
         const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(p.out + ((size_t)s * p.T + t0) * p.n_head * HD), (short)0, (int)((uint32_t)(t1 - t0) * otok_b),
-            kBufferFlags);
+            (void*)(static_cast<uint16_t*>(p.out) + ((size_t)s * p.T + t0) * p.o_tok), (short)0,
+            (int)((uint32_t)(t1 - t0) * otok_b), kBufferFlags);
 #pragma unroll
         for (int k = 0; k < NST; ++k) {
             const int r = wave * RT * 32 + k * RPI + lane / PPR;  // token r / HPK of the block, head r % HPK
@@ -1170,7 +1186,7 @@ static int window_tiles(int window, int TB) {
     return (chunks + 1) / 2;
 }
 
-template <int HD, int RT, int NW>
+template <int HD, int RT, int NW, bool F32>
 static hipError_t launch_nw(const PrefillParams& p, hipStream_t st) {
     constexpr int ROWS = NW * RT * 32;
     if (p.hpk > ROWS) return hipErrorNotSupported;
@@ -1183,20 +1199,20 @@ static hipError_t launch_nw(const PrefillParams& p, hipStream_t st) {
     // head dim 64: short windows keep all their K/V tiles in LDS (<= 3 of
     // each: 56 KB, two 4-wave workgroups per CU)
     const int wt = window_tiles(p.window, TB);
-    const bool res = HD == 64 && !p.state && wt > 0 && wt <= 3 && !kNoResidentTiles;
+    const bool res = HD == 64 && !p.state && wt > 0 && wt <= 3;
     if constexpr (HD == 64 && NW == 4) {
         if (res) {
-            if (p.ring_cap) hipLaunchKernelGGL((prefill_kernel<HD, RT, true, false, NW, 3>), grid, block, 0, st, p, n_tb, TB);
-            else hipLaunchKernelGGL((prefill_kernel<HD, RT, false, false, NW, 3>), grid, block, 0, st, p, n_tb, TB);
+            if (p.ring_cap) hipLaunchKernelGGL((prefill_kernel<HD, RT, true, false, NW, 3, F32>), grid, block, 0, st, p, n_tb, TB);
+            else hipLaunchKernelGGL((prefill_kernel<HD, RT, false, false, NW, 3, F32>), grid, block, 0, st, p, n_tb, TB);
             return hipGetLastError();
         }
     }
     if (p.state)
-        hipLaunchKernelGGL((prefill_kernel<HD, RT, false, true, NW>), grid, block, 0, st, p, n_tb, TB);
+        hipLaunchKernelGGL((prefill_kernel<HD, RT, false, true, NW, 0, F32>), grid, block, 0, st, p, n_tb, TB);
     else if (p.ring_cap)
-        hipLaunchKernelGGL((prefill_kernel<HD, RT, true, false, NW>), grid, block, 0, st, p, n_tb, TB);
+        hipLaunchKernelGGL((prefill_kernel<HD, RT, true, false, NW, 0, F32>), grid, block, 0, st, p, n_tb, TB);
     else
-        hipLaunchKernelGGL((prefill_kernel<HD, RT, false, false, NW>), grid, block, 0, st, p, n_tb, TB);
+        hipLaunchKernelGGL((prefill_kernel<HD, RT, false, false, NW, 0, F32>), grid, block, 0, st, p, n_tb, TB);
     return hipGetLastError();
 }
 
@@ -1207,11 +1223,6 @@ static hipError_t launch_nw(const PrefillParams& p, hipStream_t st) {
 // ring slots of the sliding-window kernel: the chunks of two consecutive
 // 64-token blocks, (126 + window) / 32 + 2, fit for windows up to 130
 constexpr int kSlideChunks = 10;
-#ifdef PELICA_PRE_NO_SLIDE
-constexpr bool kNoSlide = true;
-#else
-constexpr bool kNoSlide = false;
-#endif
 
 static int prefill_cus() {
     static const int n = [] {
@@ -1227,7 +1238,7 @@ static int prefill_cus() {
 // the sliding-window kernel's shapes: head dim 64, 8 heads per kv head,
 // whole-prompt launches, a window its chunk ring holds
 static bool slide_fits(const PrefillParams& p) {
-    return !kNoSlide && p.hd == 64 && p.hpk == 8 && !p.state && p.window > 0 &&
+    return p.hd == 64 && p.hpk == 8 && !p.state && p.window > 0 &&
            (126 + p.window) / 32 + 2 <= kSlideChunks;
 }
 
@@ -1248,11 +1259,11 @@ static hipError_t launch_slide(const PrefillParams& p, hipStream_t st) {
     return hipGetLastError();
 }
 
-template <int HD, int RT>
+template <int HD, int RT, bool F32>
 static hipError_t launch(const PrefillParams& p, hipStream_t st) {
-    if (HD == 64 && RT == 2 && slide_fits(p)) return launch_slide(p, st);
-    if (p.window > 0 && p.window <= 1024) return launch_nw<HD, RT, 4>(p, st);
-    return launch_nw<HD, RT, 8>(p, st);
+    if (HD == 64 && RT == 2 && !F32 && slide_fits(p)) return launch_slide(p, st);
+    if (p.window > 0 && p.window <= 1024) return launch_nw<HD, RT, 4, F32>(p, st);
+    return launch_nw<HD, RT, 8, F32>(p, st);
 }
 
 #ifdef PELICA_PTRACE
@@ -1262,11 +1273,13 @@ extern "C" int pelica_attn_debug_ptrace(void* dst, size_t bytes) {
 #endif
 
 hipError_t launch_prefill(const PrefillParams& p, hipStream_t st) {
-#ifndef PELICA_PRE_RT64
-#define PELICA_PRE_RT64 2
-#endif
-    if (p.hd == 64) return launch<64, PELICA_PRE_RT64>(p, st);
-    if (p.hd == 128) return launch<128, 1>(p, st);
+    if (p.f32) {
+        if (p.hd == 64) return launch<64, 2, true>(p, st);
+        if (p.hd == 128) return launch<128, 1, true>(p, st);
+    } else {
+        if (p.hd == 64) return launch<64, 2, false>(p, st);
+        if (p.hd == 128) return launch<128, 1, false>(p, st);
+    }
     return hipErrorNotSupported;
 }
 

@@ -5,11 +5,13 @@
 namespace pelica {
 
 struct PrefillParams {
-    const uint16_t* q;
+    const void* q;       // f16, or f32 with f32
     const uint16_t* k;
     const uint16_t* v;
     const float* sinks;
-    uint16_t* out;
+    void* out;           // f16, or f32 with f32
+    bool f32;            // f32 queries and output
+    int64_t q_tok, o_tok;  // values between consecutive query / output tokens
     const int32_t* seq_len;
     const int64_t* seq_off;
     int64_t row_stride;  // f16 values between cache rows

@@ -162,10 +162,7 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(QkvParams p) {
 
 // tokens per wave (gpt-oss 4096-token step: 1 token 34.7 us, 2 30.3, 3 30.3,
 // 4 30.0-30.8, 5 32.7, 6 33-35, 8 36.5)
-#ifndef PELICA_QKV_TPW
-#define PELICA_QKV_TPW 4
-#endif
-constexpr int kQkvTpw = PELICA_QKV_TPW;
+constexpr int kQkvTpw = 4;
 
 template <int HD>
 static void launch_hd(const QkvParams& p, bool vec, dim3 grid, hipStream_t st) {

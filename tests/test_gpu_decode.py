@@ -321,39 +321,3 @@ def test_per_kernel_timing():
     assert names.count("decode_split") == 3 and names.count("decode_combine") == 3
     assert all(ms > 0 for _, ms in recs)
     assert attn.prof_read() == []
-
-
-@pytest.mark.parametrize("cfg", [wl.C3_FULL.scaled(kv_len=20000), wl.C2, wl.C1,
-                                 wl.AttnConfig("fwin", "decode", 64, 8, 64, 9000, q_tokens=3, n_seq=2, window=3000,
-                                               sinks=True, seed=61)],
-                         ids=lambda c: c.name)
-def test_fused_merge_variant(monkeypatch, cfg):
-    # the opt-in in-kernel split merge (PELICA_ATTN_FUSE=1, a measured
-    # alternative to the combine launch) gives the combine's result within
-    # fp32 reassociation, on a zero-filled workspace reused across calls
-    inp = wl.make_inputs(cfg, "cuda")
-    kw = dict(n_kv=cfg.n_kv, kv_len=inp.kv_len, sinks=inp.sinks, window=cfg.window)
-    ref = attn.decode(inp.q, inp.k, inp.v, **kw)
-    torch.cuda.synchronize()
-    try:
-        monkeypatch.setenv("PELICA_ATTN_FUSE", "1")
-        attn.reload_tuning()
-        desc = attn.make_desc(cfg.n_head, cfg.n_kv, cfg.hd, n_seq=cfg.n_seq, q_tokens=cfg.q_tokens,
-                              kv_len=inp.kv_len, window=cfg.window)
-        ws = attn.new_workspace(desc)
-        print(f"[case] fused merge {cfg.name}", flush=True)
-        outs = [attn.decode(inp.q, inp.k, inp.v, workspace=ws, **kw) for _ in range(3)]
-        torch.cuda.synchronize()
-        parts = attn.decode_partials(inp.q, inp.k, inp.v, n_kv=cfg.n_kv, kv_len=inp.kv_len, window=cfg.window,
-                                     workspace=ws)
-        torch.cuda.synchronize()
-    finally:
-        monkeypatch.delenv("PELICA_ATTN_FUSE")
-        attn.reload_tuning()
-    for o in outs:
-        assert np.abs(as_f64(o) - as_f64(ref)).max() < 2e-6
-    assert torch.equal(outs[0], outs[2])
-    merged = attn.partials_merge_batch(parts.reshape(1, -1, cfg.n_head, cfg.hd + 2).contiguous(), sinks=inp.sinks)
-    torch.cuda.synchronize()
-    assert np.abs(as_f64(merged).reshape(ref.shape) - as_f64(ref)).max() < 2e-6
-    assert_close(as_f64(outs[0]), as_f64(oracle_run(inp)), what=f"fused {cfg.name}")

@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     lib = attn.load_library()
     for name in header_functions():
         assert hasattr(lib, name), name
-    assert lib.pelica_attn_version() == 1
+    assert lib.pelica_attn_version() == 2
 
 
 def _desc(**kw):
@@ -184,3 +184,67 @@ def test_package_exports_every_public_binding():
     assert public <= set(pelica_amd.__all__), sorted(public - set(pelica_amd.__all__))
     for n in pelica_amd.__all__:
         assert getattr(pelica_amd, n) is getattr(attn, n)
+
+
+def test_descriptor_layout_matches_the_c_header(tmp_path):
+    # the ctypes mirror and the C struct agree field by field (gcc on the header)
+    src = tmp_path / "layout.c"
+    fields = [f for f, _ in attn.AttnDesc._fields_]
+    body = "".join(f'printf("{f} %zu\\n", offsetof(PelicaAttnDesc, {f}));\n' for f in fields)
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "pelica_attn.h"\n'
+                   'int main(void) {\n' + body + 'printf("size %zu\\n", sizeof(PelicaAttnDesc));\nreturn 0;\n}\n')
+    exe = tmp_path / "layout"
+    import subprocess
+
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), "-o", str(exe), str(src)], check=True)
+    out = dict(line.split() for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                       check=True).stdout.splitlines())
+    for f in fields:
+        assert int(out[f]) == getattr(attn.AttnDesc, f).offset, f
+    assert int(out["size"]) == ctypes.sizeof(attn.AttnDesc)
+
+
+@pytest.mark.parametrize("field,value", [
+    ("q_token_stride", 64 * 64 - 4),     # below a token's heads
+    ("q_token_stride", 64 * 64 + 2),     # rows no longer 16-byte aligned
+    ("q_token_stride", 1 << 20),         # past the kernels' 32-bit block offsets
+    ("out_token_stride", 64 * 64 + 1),
+])
+def test_token_strides_are_validated(field, value):
+    lib = attn.load_library()
+    d = _desc(q_tokens=4)
+    setattr(d, field, value)
+    for rc in (lib.pelica_attn_decode(ctypes.byref(d), 16, 16, 16, None, 16, None, 0, None),
+               lib.pelica_attn_decode_partials(ctypes.byref(d), 16, 16, 16, 16, None, 0, None),
+               lib.pelica_attn_prefill_f32(ctypes.byref(d), 16, 16, 16, None, 16, None)):
+        assert rc == attn.EINVAL and field.encode() in lib.pelica_attn_last_error()
+    # f16 prefill rows: a multiple of 8 values (4 is enough for f32 rows)
+    d = _desc(q_tokens=4)
+    setattr(d, field, 64 * 64 + 4)
+    assert lib.pelica_attn_prefill(ctypes.byref(d), 16, 16, 16, None, 16, None) == attn.EINVAL
+    assert field.encode() in lib.pelica_attn_last_error()
+
+
+def test_token_stride_of_views():
+    import torch
+
+    rows = torch.zeros(2, 3, (64 + 2 * 8) * 64)
+    q = rows[..., :64 * 64].view(2, 3, 64, 64)
+    assert attn.token_stride(q) == (64 + 2 * 8) * 64
+    assert attn.token_stride(torch.zeros(2, 3, 64, 64)) == 0
+    assert attn.token_stride(rows[:, :1, :64 * 64].view(2, 1, 64, 64)) == (64 + 2 * 8) * 64 * 3
+    with pytest.raises(attn.AttnError):
+        attn.token_stride(torch.zeros(2, 3, 64, 128)[..., :64])
+
+
+def test_key_range_arguments():
+    lib = attn.load_library()
+    f = lib.pelica_attn_decode_partials_range
+    d = _desc(q_tokens=4, kv_len=20000)
+    assert f(ctypes.byref(d), 16, 16, 16, 0, 0, 16, None, 0, None) == attn.EINVAL           # empty
+    assert f(ctypes.byref(d), 16, 16, 16, 100, 20001, 16, None, 0, None) == attn.EINVAL     # past kv_len
+    assert f(ctypes.byref(d), 16, 16, 16, -1, 50, 16, None, 0, None) == attn.EINVAL         # negative
+    assert f(ctypes.byref(d), 16, 16, 16, 0, 50, None, None, 0, None) == attn.EINVAL        # no parts
+    d2 = _desc(q_tokens=4, kv_len=20000, n_seq=2)
+    assert f(ctypes.byref(d2), 16, 16, 16, 0, 50, 16, None, 0, None) == attn.EINVAL
+    assert b"one sequence" in lib.pelica_attn_last_error()
