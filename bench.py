@@ -531,11 +531,11 @@ def dtrace_summary(args):
         t0 = float(w[:, 0].min())
         rel = lambda col: (w[:, col].astype(np.float64) - t0) / 100.0
         q = lambda a: [round(float(np.percentile(a, p)), 2) for p in (10, 50, 90)]
-        ok = lambda col: w[:, col] > 0
+        ok = lambda col: w[:, col] >= w[:, 0]  # (stamps of this call: not before the wave's own start)
         out = {"config": name, "waves": int(len(w)), "pct": "p10/p50/p90 us from the first wave's start"}
-        last = w[:, 6] > 0  # waves that wrote a result (the merging wave of each head)
-        for col, key in ((0, "start"), (1, "first_k_landed"), (2, "v0_landed"), (3, "v1_landed"), (4, "loop_end"),
-                         (6, "end")):
+        last = ok(6)  # waves that wrote a result (the merging wave of each head)
+        for col, key in ((0, "start"), (1, "first_k_landed"), (2, "v0_landed"), (3, "v1_landed_or_b0_issued"),
+                         (4, "loop_end"), (6, "end")):
             m = ok(col)
             if m.any():
                 out[key] = q(rel(col)[m])

@@ -217,9 +217,13 @@ int plan_decode(const PelicaAttnDesc* d, DecodePlan* pl, int kr_len = 0) {
     splits(nw, &split_keys, &n_slot);
     // Small head-dim-128 calls: with 4-wave workgroups the grid would not
     // reach every CU (a CU pulls ~22 GB/s at most here), so split the keys
-    // twice as finely over 2-wave workgroups (OLMoE, Qwen3 decode: ~10 %).
+    // four times as finely over one-wave workgroups: every wave writes its
+    // own split's partials, with no merge between waves after its last
+    // block (OLMoE 2K / Qwen3 8K decode: split kernel 7.45 -> 6.97 /
+    // 7.68 -> 6.88 us against 2-wave workgroups, whole call 10.14 -> 9.95
+    // / 10.87 -> 10.45 us).
     if (!big && d->hd == 128 && (long long)n_slot * groups < device_cus()) {
-        nw = 2;
+        nw = 1;
         splits(nw, &split_keys, &n_slot);
     }
     // Window layers: when the keys any row sees fit one workgroup (each wave

@@ -275,8 +275,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     constexpr int ROWS = RT * 16;
     constexpr bool EARLY_V = HD == 64 && !SK;
     // f16 parts (hi + lo) of Q and P: packed (PK: hi in columns 0-7, lo in
-    // 8-15, one MFMA), or two separate passes
+    // 8-15, one MFMA), or separate passes: NP of Q, NPP of P
     constexpr int NP = PK ? 1 : 2;
+    constexpr int NPP = PK ? 1 : 2;
     constexpr int BUF = 64 * HD * 2;                   // bytes of one 64-key K or V block
     constexpr int STATE = DT * RT * 64 * 16 + RT * 64 * 8;  // bytes of one wave's (O, m, l)
     // LDS per wave: a K and a V block buffer, filled straight from HBM;
@@ -394,6 +395,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     if (QFIRST) {
         issue_k(0, true);
         issue_v(0, true);
+        if (nb == 1) DTRACE(3);  // (one-block waves: stamp 3 = block 0 requested)
     }
 
     // ---- f16 parts (hi[, lo]) of the queries in base 2 ----
@@ -517,7 +519,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
                         if (key < lor[rt] || key > posr[rt]) sc[kt][rt][i] = -INFINITY;
                 }
         }
-        half8 pf[NP][RT][2];
+        half8 pf[NPP][RT][2];
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
             float bm = -INFINITY;
@@ -543,7 +545,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
                         pf[0][rt][kt >> 1][e] = c16 < 8 ? hi : (_Float16)(pe - (float)hi);
                     } else {
                         pf[0][rt][kt >> 1][e] = hi;
-                        if (NP > 1) pf[NP - 1][rt][kt >> 1][e] = (_Float16)(pe - (float)hi);
+                        if (NPP > 1) pf[NPP - 1][rt][kt >> 1][e] = (_Float16)(pe - (float)hi);
                     }
                 }
             l[rt] = l[rt] * c + ls;
@@ -555,7 +557,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
         // here; otherwise the compiler sinks the exp2s below the wait
         if constexpr (EARLY_V) {
 #pragma unroll
-            for (int pp = 0; pp < NP; ++pp)
+            for (int pp = 0; pp < NPP; ++pp)
 #pragma unroll
                 for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -584,7 +586,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
                                  : cat8(lds_read_tr(v_elem<HD>(vb, k0, d0)), lds_read_tr(v_elem<HD>(vb, k0 + 16, d0)));
             }
 #pragma unroll
-            for (int pp = 0; pp < NP; ++pp)
+            for (int pp = 0; pp < NPP; ++pp)
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -1026,9 +1028,9 @@ hipError_t launch_decode(const DecodeParams& p, int rt, int nw, hipStream_t st) 
     } else if (p.hd == 128 && nw == 4 && p.wg_heads == 1) {
         if (rt == 1) return launch_k<128, 1, 4, 1>(p, st);
         if (rt == 2) return launch_k<128, 2, 4, 1>(p, st);
-    } else if (p.hd == 128 && nw == 2 && p.wg_heads == 1) {
-        if (rt == 1) return launch_k<128, 1, 2, 1>(p, st);
-        if (rt == 2) return launch_k<128, 2, 2, 1>(p, st);
+    } else if (p.hd == 128 && nw == 1 && p.wg_heads == 1) {
+        if (rt == 1) return launch_k<128, 1, 1, 1>(p, st);
+        if (rt == 2) return launch_k<128, 2, 1, 1>(p, st);
     }
     return hipErrorInvalidValue;
 }
