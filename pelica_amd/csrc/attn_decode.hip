@@ -464,13 +464,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     float4v sc[4][RT];
     // after_reads: runs once the block's K operands are in registers (the
     // K buffer is then free for the next block's loads)
-    auto qk = [&](auto&& after_reads) {
+    // The block's first 32 keys come with the first half of its loads: their
+    // QK^T runs once that half has landed (the wait before qk), the second
+    // half's after mid_wait() — the products overlap the block's arrival.
+    auto qk = [&](auto&& mid_wait, auto&& after_reads) {
         half8 kc[4][DS];
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-            for (int ds = 0; ds < DS; ++ds) kc[kt][ds] = load16(kread[ds] + kt * 16 * (HD * 2));
-        after_reads();
         // independent accumulators per (part, key tile, row tile); the
         // k-steps run outermost so consecutive MFMAs do not depend on each other
         float4v acc[NP][4][RT];
@@ -481,13 +479,23 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
 #pragma unroll
                 for (int rt = 0; rt < RT; ++rt) acc[pp][kt][rt] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ds = 0; ds < DS; ++ds)
+        for (int half = 0; half < 2; ++half) {
+            if (half == 1) mid_wait();
 #pragma unroll
-            for (int pp = 0; pp < NP; ++pp)
+            for (int kt = 2 * half; kt < 2 * half + 2; ++kt)
 #pragma unroll
-                for (int kt = 0; kt < 4; ++kt)
+                for (int ds = 0; ds < DS; ++ds) kc[kt][ds] = load16(kread[ds] + kt * 16 * (HD * 2));
+            if (half == 1) after_reads();
 #pragma unroll
-                    for (int rt = 0; rt < RT; ++rt) acc[pp][kt][rt] = mfma16(kc[kt][ds], qf[pp][rt][ds], acc[pp][kt][rt]);
+            for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+                for (int pp = 0; pp < NP; ++pp)
+#pragma unroll
+                    for (int kt = 2 * half; kt < 2 * half + 2; ++kt)
+#pragma unroll
+                        for (int rt = 0; rt < RT; ++rt)
+                            acc[pp][kt][rt] = mfma16(kc[kt][ds], qf[pp][rt][ds], acc[pp][kt][rt]);
+        }
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
@@ -505,7 +513,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     // 32 more VGPRs fit): the block's V^T operands are then all read and
     // after_vreads() runs before the PV MFMAs (the V buffer is free for the
     // next block's loads before PV, not after it).
-    auto softmax_pv = [&](int kb, auto&& wait_v, auto&& after_vreads) {
+    // wait_v_half(): keys 0-31 of the block's V landed (the first half of
+    // its loads); wait_v(): all of it
+    auto softmax_pv = [&](int kb, auto&& wait_v_half, auto&& wait_v, auto&& after_vreads) {
         const _Float16* vb = reinterpret_cast<const _Float16*>(vlds);
         // mask (blocks at a range boundary only): row r sees keys [lor, posr]
         if (kb < lo_hi || kb + 63 > pos_lo) {
@@ -555,36 +565,28 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
         // the softmax stays ahead of the wait for V (it needs only the
         // scores): the empty asm takes P as an operand, so P is computed
         // here; otherwise the compiler sinks the exp2s below the wait
-        if constexpr (EARLY_V) {
 #pragma unroll
-            for (int pp = 0; pp < NPP; ++pp)
+        for (int pp = 0; pp < NPP; ++pp)
 #pragma unroll
-                for (int rt = 0; rt < RT; ++rt)
+            for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-                    for (int u = 0; u < 2; ++u) __asm__ volatile("" : "+v"(pf[pp][rt][u]));
-        }
-        wait_v();
-        half8 va_all[EARLY_V ? 2 : 1][DT];
-        if constexpr (EARLY_V) {
-#pragma unroll
-            for (int u = 0; u < 2; ++u)
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) {
-                    const int k0 = 32 * u + 4 * g + (c16 >> 2), d0 = 16 * dt + 4 * (c16 & 3);
-                    va_all[u][dt] = cat8(lds_read_tr(v_elem<HD>(vb, k0, d0)), lds_read_tr(v_elem<HD>(vb, k0 + 16, d0)));
-                }
-            after_vreads();
-        }
-        // O^T += V^T P^T; the dim tiles are independent accumulators
+                for (int u = 0; u < 2; ++u) __asm__ volatile("" : "+v"(pf[pp][rt][u]));
+        // O^T += V^T P^T over keys 32 u .. 32 u + 31; the dim tiles are
+        // independent accumulators.  Keys 0-31 go as soon as the first half
+        // of V has landed.  EARLY_V: each half's V^T operands are all read
+        // before its MFMAs, and the next block's V goes out after the
+        // second half's reads.
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
+            if (u == 0) wait_v_half();
+            else wait_v();
             half8 va[DT];
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
                 const int k0 = 32 * u + 4 * g + (c16 >> 2), d0 = 16 * dt + 4 * (c16 & 3);
-                va[dt] = EARLY_V ? va_all[EARLY_V ? u : 0][dt]
-                                 : cat8(lds_read_tr(v_elem<HD>(vb, k0, d0)), lds_read_tr(v_elem<HD>(vb, k0 + 16, d0)));
+                va[dt] = cat8(lds_read_tr(v_elem<HD>(vb, k0, d0)), lds_read_tr(v_elem<HD>(vb, k0 + 16, d0)));
             }
+            if (EARLY_V && u == 1) after_vreads();
 #pragma unroll
             for (int pp = 0; pp < NPP; ++pp)
 #pragma unroll
@@ -606,14 +608,19 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kDecode
     // are untracked by the compiler, which would otherwise wait for every
     // outstanding load (K(i+1) too) before PV's transposing V reads.
     for (int i = 0; i < nb; ++i) {
-        wait_vm<VPL>();  // K(i) landed
+        wait_vm<VPL + VPL / 2>();  // the first half of K(i) landed
         if (i == 0) DTRACE(1);
-        qk([&] {
-            wait_lgkm0();
-            if (i + 1 < nb) issue_k(i + 1, false);
-        });
+        qk([&] { wait_vm<VPL>(); },  // K(i) landed
+           [&] {
+               wait_lgkm0();
+               if (i + 1 < nb) issue_k(i + 1, false);
+           });
         softmax_pv(
             blk(i),
+            [&] {  // the first half of V(i) landed (K(i+1) may be in flight behind it)
+                if (i + 1 < nb) wait_vm<VPL + VPL / 2>();
+                else wait_vm<VPL / 2>();
+            },
             [&] {
                 if (i + 1 < nb) wait_vm<VPL>();  // V(i) landed
                 else wait_vm<0>();
