@@ -542,7 +542,7 @@ def dtrace_summary(args):
         both = ok(3) & ok(4)
         if both.any():  # per wave: the last block's V landed -> its PV done
             out["v1_landed_to_loop_end_us"] = q(((w[:, 4].astype(np.float64) - w[:, 3]) / 100.0)[both])
-        if last.any():
+        if (last & ok(5)).any():  # (workgroups of more than one wave per head)
             out["merging_wave_loop_to_merged_us"] = q(((w[:, 5].astype(np.float64) - w[:, 4]) / 100.0)[last & ok(5)])
             out["merging_wave_merged_to_end_us"] = q(((w[:, 6].astype(np.float64) - w[:, 5]) / 100.0)[last & ok(5)])
         out["last_end_us"] = round(float(rel(6)[ok(6)].max()), 2) if ok(6).any() else None
