@@ -248,3 +248,21 @@ def test_key_range_arguments():
     d2 = _desc(q_tokens=4, kv_len=20000, n_seq=2)
     assert f(ctypes.byref(d2), 16, 16, 16, 0, 50, 16, None, 0, None) == attn.EINVAL
     assert b"one sequence" in lib.pelica_attn_last_error()
+
+
+def test_recorded_traffic_follows_the_kernel_sources(tmp_path, monkeypatch):
+    # bench.py reports roofline.traffic from the committed counter summary
+    # only while the kernel's sources hash as they did when it was measured
+    import bench
+
+    lines = [ln.split() for ln in open(bench.TRAFFIC_PROFILE).read().splitlines() if ln.startswith("traffic ")]
+    assert {f[1] for f in lines} >= {"c3_gptoss_decode_full", "c4_gptoss_prefill_full"}
+    for f in lines:
+        assert len(f) == 4 and int(f[2]) > 0 and f[3].startswith("src=")
+        got, note = bench.recorded_traffic(f[1])
+        fresh = f[3] == "src=" + bench.sources_hash(bench.TRAFFIC_KERNELS[f[1]][1])
+        assert (got == int(f[2])) == fresh, note
+    stale = tmp_path / "t.md"
+    stale.write_text("traffic c3_gptoss_decode_full 123 src=000000000000\n")
+    monkeypatch.setattr(bench, "TRAFFIC_PROFILE", str(stale))
+    assert bench.recorded_traffic("c3_gptoss_decode_full")[0] is None
