@@ -307,6 +307,7 @@ int plan_mla(const PelicaAttnDesc* d, DecodePlan* pl) {
     pl->n_slot = n_slot;
     pl->wg_heads = 1;
     pl->nw = 4;
+    pl->sk = false;
     const size_t n_part = (size_t)d->n_seq * R * n_slot;
     pl->ctr_bytes = 0;
     pl->ml_bytes = (n_part * 2 * 4 + 255) & ~(size_t)255;
