@@ -869,7 +869,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
     if (len < p.T || len <= 0) return;
     const int t = r / p.hpk, h = kvh * p.hpk + r % p.hpk;
     int c0, c1;  // the splits that hold keys of this row
-    if (p.sk) {
+    if (p.sk_grid > 0) {
         // stream-K: every piece of the row's segment (rows with no key in a
         // piece have an empty partial there); the split kernel records the
         // count.  (Loading every workspace slot before the count arrives was
