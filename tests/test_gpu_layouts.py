@@ -196,3 +196,83 @@ def test_mla_with_token_strides():
     torch.cuda.synchronize()
     assert torch.equal(xo[..., :H * 512].reshape(dense.shape), dense)
     assert torch.all(xo[..., H * 512:] == 0)
+
+
+def _widen(t, extra):
+    """t [n_seq, T, H, hd] copied into token rows of H*hd + extra values; the view."""
+    n_seq, T, H, hd = t.shape
+    rows = torch.full((n_seq, T, H * hd + extra), 5.0, dtype=t.dtype, device=t.device)
+    rows[..., :H * hd] = t.reshape(n_seq, T, H * hd)
+    return rows, rows[..., :H * hd].view(n_seq, T, H, hd)
+
+
+@pytest.mark.parametrize("hd,n_head,n_kv,T,n_seq,kv_len", [(128, 32, 4, 4, 12, 6000), (64, 64, 8, 1, 9, 5000)])
+def test_strided_ragged_stream_k(hd, n_head, n_kv, T, n_seq, kv_len):
+    # ragged batches (stream-K) reading strided queries and writing strided rows
+    from pelica_amd import workloads as wl
+    from tests.gpu_util import oracle_run
+
+    cfg = wl.AttnConfig("sk-strided", "decode", n_head, n_kv, hd, kv_len, q_tokens=T, n_seq=n_seq,
+                        ragged=(T, kv_len), sinks=hd == 64, seed=31 + n_seq)
+    inp = wl.make_inputs(cfg, "cuda")
+    kw = dict(n_kv=n_kv, kv_len=inp.kv_len, sinks=inp.sinks, seq_kv_len=inp.seq_len, seq_kv_offset=inp.seq_off)
+    dense = attn.decode(inp.q, inp.k, inp.v, **kw)
+    _, q = _widen(inp.q, 96)
+    xo, out = _widen(torch.zeros_like(inp.q), 32)
+    print(f"[case] strided stream-K hd{hd} T{T} n_seq{n_seq}", flush=True)
+    attn.decode(q, inp.k, inp.v, out=out, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(out, dense)
+    assert torch.all(xo[..., n_head * hd:] == 5.0)
+    assert_close(as_f64(out), as_f64(oracle_run(inp)), what="strided stream-K")
+
+
+@pytest.mark.parametrize("hd,n_head,n_kv,T,L,window,ring,n_seq", [
+    (128, 32, 4, 150, 150, 0, 0, 1),       # head dim 128
+    (128, 32, 4, 96, 400, 64, 0, 1),       # window, prefix
+    (64, 64, 8, 200, 900, 128, 384, 1),    # ring cache of a window layer
+    (64, 16, 4, 70, 300, 0, 0, 3),         # ragged sequences
+])
+def test_f32_prefill_shapes(hd, n_head, n_kv, T, L, window, ring, n_seq):
+    # the f32 form against the f32 oracle, on the layouts of the f16 tests
+    from pelica_amd import workloads as wl
+
+    cfg = wl.AttnConfig("pf32", "decode", n_head, n_kv, hd, L, q_tokens=T, n_seq=n_seq, window=window,
+                        ragged=(T, L) if n_seq > 1 else None, sinks=True, seed=41 + hd + T)
+    inp = wl.make_inputs(cfg, "cuda")
+    k, v = inp.k, inp.v
+    kw = dict(n_kv=n_kv, kv_len=inp.kv_len, sinks=inp.sinks, window=window)
+    if n_seq > 1:
+        kw.update(seq_kv_len=inp.seq_len, seq_kv_offset=inp.seq_off)
+    if ring:
+        kr = torch.zeros(ring, n_kv, hd, dtype=torch.float16, device="cuda")
+        vr = torch.zeros_like(kr)
+        idx = torch.arange(L - ring, L, device="cuda")
+        kr[idx % ring] = inp.k[idx]
+        vr[idx % ring] = inp.v[idx]
+        k, v = kr, vr
+        kw.update(ring_cap=ring)
+    print(f"[case] f32 prefill hd{hd} T{T} L{L} window{window} ring{ring} n_seq{n_seq}", flush=True)
+    got = attn.prefill(inp.q, k, v, **kw)
+    torch.cuda.synchronize()
+    ref = orc.attention(inp.q.cpu().numpy(), to_np_f16(inp.k), to_np_f16(inp.v), n_kv=n_kv, kv_len=inp.kv_len,
+                        seq_kv_len=inp.seq_len.cpu().numpy(), seq_kv_offset=inp.seq_off.cpu().numpy(),
+                        sinks=inp.sinks.cpu().numpy(), window=window)
+    assert got.dtype == torch.float32
+    assert_close(as_f64(got), ref.astype(np.float64), what="f32 prefill")
+
+
+def test_far_rows_head_dim_128():
+    # the key-range pass at Qwen3's shape (32 q heads, 4 kv heads, 4 drafts)
+    from pelica_amd import workloads as wl
+
+    cfg = wl.AttnConfig("far128", "decode", 32, 4, 128, 9000, q_tokens=4, seed=51)
+    inp = wl.make_inputs(cfg, "cuda")
+    res = 6137
+    kw = dict(n_kv=4, kv_len=9000)
+    a = attn.decode_partials_range(inp.q, inp.k[:res].clone(), inp.v[:res].clone(), key_begin=0, key_end=res, **kw)
+    b = attn.decode_partials_range(inp.q, inp.k[res:].clone(), inp.v[res:].clone(), key_begin=res, key_end=9000, **kw)
+    out = attn.partials_merge_batch(torch.stack([a.reshape(4, 32, 130), b.reshape(4, 32, 130)]).contiguous())
+    torch.cuda.synchronize()
+    ref = orc.attention(inp.q.cpu().numpy(), to_np_f16(inp.k), to_np_f16(inp.v), n_kv=4, kv_len=9000)
+    assert_close(as_f64(out).reshape(ref.shape), ref.astype(np.float64), what="far rows hd128")
