@@ -276,3 +276,38 @@ def test_far_rows_head_dim_128():
     torch.cuda.synchronize()
     ref = orc.attention(inp.q.cpu().numpy(), to_np_f16(inp.k), to_np_f16(inp.v), n_kv=4, kv_len=9000)
     assert_close(as_f64(out).reshape(ref.shape), ref.astype(np.float64), what="far rows hd128")
+
+
+def test_strided_calls_in_graph_replays():
+    # the call sites' layouts recorded into a HIP graph give the eager result
+    # on every replay, with unrelated eager work between the replays
+    T, L = 4, 5000
+    act, kc, vc, sinks, table = _chain_inputs(T, L, seed=61)
+    _step_before(act, kc, vc, table, T, L)
+    q = _q_view(act, T)
+    desc = attn.make_desc(N_HEAD, N_KV, HD, q_tokens=T, kv_len=L, q_token_stride=QKV_ROWS, out_token_stride=ATTW)
+    ws = attn.new_workspace(desc)
+    xo, out = _out_rows(T, torch.float32)
+    attn.decode(q, kc, vc, n_kv=N_KV, kv_len=L, sinks=sinks, out=out, workspace=ws)
+    eager_dec = out.clone()
+    Tp = 160
+    actp, kp, vp, sp, tp = _chain_inputs(Tp, Tp, seed=62)
+    _step_before(actp, kp, vp, tp, Tp, Tp)
+    qp = _q_view(actp, Tp)
+    xp, outp = _out_rows(Tp, torch.float32)
+    attn.prefill(qp, kp, vp, n_kv=N_KV, sinks=sp, window=128, out=outp)
+    eager_pre = outp.clone()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        attn.decode(q, kc, vc, n_kv=N_KV, kv_len=L, sinks=sinks, out=out, workspace=ws)
+        attn.prefill(qp, kp, vp, n_kv=N_KV, sinks=sp, window=128, out=outp)
+    for _ in range(3):
+        out.zero_()
+        outp.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager_dec) and torch.equal(outp, eager_pre)
+        _check_rest(xo)
+        _check_rest(xp)
+        _ = (act * 2).sum().item()  # unrelated eager work between replays
