@@ -86,6 +86,8 @@ def parse():
     ap.add_argument("--traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of "
                          "--profile copy,<configs> into the lines the roofline's traffic is read from")
+    ap.add_argument("--gemm", action="store_true",
+                    help="calibration: the f16 rate of the platform's GEMM (torch.matmul, hipBLASLt) on this GPU")
     ap.add_argument("--ptrace", default="",
                     help="comma list of prefill configs: summarise the prefill kernel's per-wave stamps "
                          "(needs a library built with -DPELICA_PTRACE, loaded through PELICA_ATTN_LIB)")
@@ -587,6 +589,30 @@ def traffic_summary(args):
         print(f"traffic {cfg} {int(round(fb + wb))} src={sources_hash(kind)}")
 
 
+def gemm_rate():
+    """Dense f16 GEMM rate of the platform library on this GPU (square
+    problems, HIP events over 20 back-to-back calls): the MFMA rate a
+    GEMM-only kernel reaches under the chip's power and clock limits."""
+    import torch
+
+    for n in (8192, 16384):
+        a = torch.randn(n, n, dtype=torch.float16, device="cuda")
+        b = torch.randn(n, n, dtype=torch.float16, device="cuda")
+        for _ in range(3):
+            a @ b
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(20):
+            a @ b
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / 20
+        tf = 2 * n ** 3 / (ms * 1e-3) / 1e12
+        print(json.dumps({"gemm": f"f16 {n}x{n}x{n}", "us": round(ms * 1e3, 1), "TFLOPs": round(tf, 1),
+                          "frac_of_2500": round(tf / F16_PEAK_TFLOPS, 3)}), flush=True)
+
+
 def main():
     args = parse()
     if args.traffic:
@@ -600,6 +626,8 @@ def main():
     from pelica_amd import workloads as wl
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.gemm:
+        return gemm_rate()
     if args.profile:
         return profile_only(args)
     if args.ptrace:
